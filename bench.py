@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention operator (one GPU).
+
+Step = one causal GQA prefill forward with LSE on the Llama-3-8B attention shape (B=4, Hq=32, Hkv=8,
+S=2048, D=128, bf16), inputs resident in HBM.  ``value`` is algorithmic TFLOP/s (visible pairs only:
+4*B*Hq*D*S(S+1)/2) over the timed steps.  Also reported, each on its own synthetic inputs: split-KV
+decode HBM GB/s (B=64, Hq=32, Hkv=8, D=128, lengths U[512, 8192]), the ring step (4 blocks + LSE
+merge), MMDiT joint attention in bf16 and fp8, and the fp32 causal MHA case.  The CPU baseline is
+libtorch's CPU SDPA (the call SdpaOp::Compute makes on a CPU mesh) on a bounded sample of the same
+prefill, timed on this host, and compared with the GPU output of the same rows.
+
+Prints ONE JSON line on stdout; human-readable detail goes to stderr.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16 = 2.5e15   # MI355X dense bf16 MFMA, FLOP/s (published)
+PEAK_FP8 = 5.0e15    # MI355X dense fp8 MFMA
+PEAK_HBM = 8.0e12    # MI355X HBM3E, B/s
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def causal_flops(B, Hq, S, D):
+    return 4 * B * Hq * D * S * (S + 1) // 2
+
+
+class Timer:
+    """HIP events on the stream the kernels launch on (torch's current stream)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, fn, reps, warmup=2, flush=None):
+        t = self.torch
+        for _ in range(warmup):
+            fn()
+        t.cuda.synchronize()
+        times = []
+        for _ in range(reps):
+            if flush is not None:
+                flush()
+            s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            e.synchronize()
+            times.append(s.elapsed_time(e) * 1e-3)
+        return float(np.median(times)), float(np.mean(times))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extras", action="store_true", help="only the headline prefill")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the attention "
+              "operator is not sharded across GPUs here.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import dtorch_amd.nn.functional as F
+
+    dev = torch.device("cuda:0")
+    pk = F.device_peaks(0)
+    log(f"device {pk.arch}: {pk.cu_count} CUs @ {pk.clock_hz / 1e9:.2f} GHz -> bf16 {pk.bf16_flops / 1e15:.2f} "
+        f"PFLOP/s, fp8 {pk.fp8_flops / 1e15:.2f} PFLOP/s (computed); published peaks used: bf16 2.5, fp8 5.0 "
+        f"PFLOP/s, HBM 8.0 TB/s")
+    timer = Timer(torch)
+
+    # ---------------------------------------------------------------- headline: Llama prefill
+    B, Hq, Hkv, S, D = 4, 32, 8, 2048, 128
+    rng = np.random.default_rng(0)
+    qn = rng.standard_normal((B, Hq, S, D), dtype=np.float32)
+    kn = rng.standard_normal((B, Hkv, S, D), dtype=np.float32)
+    vn = rng.standard_normal((B, Hkv, S, D), dtype=np.float32)
+    q, k, v = (torch.from_numpy(x).to(torch.bfloat16).to(dev) for x in (qn, kn, vn))
+    flops = causal_flops(B, Hq, S, D)
+
+    def step():
+        return F.scaled_dot_product_attention_with_lse(q, k, v, is_causal=True, enable_gqa=True)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for s_, e_ in evs:
+        s_.record()
+        out = step()
+        e_.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern = [s_.elapsed_time(e_) * 1e-3 for s_, e_ in evs]
+    ms_per_step = wall / args.steps * 1e3
+    value = flops / (wall / args.steps) / 1e12
+    k_avg = float(np.mean(kern))
+    achieved = flops / k_avg / 1e12
+    log(f"C2 prefill causal GQA bf16: {ms_per_step:.3f} ms/step wall, kernel avg {k_avg * 1e6:.1f} us -> "
+        f"{achieved:.1f} TFLOP/s ({100 * achieved * 1e12 / PEAK_BF16:.1f}% of bf16 peak)")
+
+    result = {
+        "metric": "prefill attn TFLOP/s (MFMA util %) + decode attn HBM GB/s, 1xMI355X",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,1) from numpy default_rng(0), cast to bf16 (extras: torch.randn on device)",
+        "config": {"workload": "Llama-3-8B-shape causal GQA prefill attention with LSE", "B": B, "Hq": Hq,
+                   "Hkv": Hkv, "S": S, "D": D, "causal": True, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": None,
+                     "kernel": "prefill_fwd_kernel<bf16,128,1,causal>",
+                     "work_per_launch": f"{flops} FLOP (4*B*Hq*D*S(S+1)/2)"},
+    }
+    del step
+
+    extras = {}
+    if not args.no_extras:
+        flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+
+        def flush():
+            flush_buf.zero_()
+
+        # C3 decode
+        Bd, Hqd, Hkvd, Smax, Dd = 64, 32, 8, 8192, 128
+        g = torch.Generator(device=dev).manual_seed(0)
+        qd = torch.randn(Bd, Hqd, 1, Dd, device=dev, generator=g).to(torch.bfloat16)
+        kc = torch.randn(Bd, Hkvd, Smax, Dd, device=dev, generator=g).to(torch.bfloat16)
+        vc = torch.randn(Bd, Hkvd, Smax, Dd, device=dev, generator=g).to(torch.bfloat16)
+        lens_np = np.random.default_rng(0).integers(512, 8192, size=Bd, endpoint=True).astype(np.int32)
+        lens = torch.from_numpy(lens_np).to(dev)
+        tot = int(lens_np.sum())
+        dbytes = 4096 * tot + Bd * Hqd * Dd * 2 * 2 + Bd * Hqd * 4
+        med, mean = timer.run(lambda: F.decode_attention(qd, kc, vc, lens), reps=20, flush=flush)
+        gbs = dbytes / med / 1e9
+        extras["decode_c3"] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs * 1e9 / PEAK_HBM, 4),
+                               "us": round(med * 1e6, 1), "bytes": dbytes, "sum_len": tot}
+        log(f"C3 decode: {med * 1e6:.1f} us, {gbs:.0f} GB/s ({100 * gbs * 1e9 / PEAK_HBM:.1f}% of HBM)")
+        del kc, vc, qd
+
+        # C4 ring step: 4 blocks (1 causal diagonal + 3 full) + merge
+        C = 4096
+        q4 = torch.randn(1, 32, C, 128, device=dev, generator=g).to(torch.bfloat16)
+        k4 = [torch.randn(1, 8, C, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(4)]
+        v4 = [torch.randn(1, 8, C, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(4)]
+        blocks = []
+
+        def ring_blocks():
+            blocks.clear()
+            for c in range(4):
+                blocks.append(F.scaled_dot_product_attention_with_lse(
+                    q4, k4[c], v4[c], is_causal=(c == 3), enable_gqa=True, q_offset=3 * C, k_offset=c * C))
+
+        rflops = 3 * (4 * 32 * 128 * C * C) + causal_flops(1, 32, C, 128)
+        med, _ = timer.run(ring_blocks, reps=5)
+        extras["ring_c4_blocks"] = {"TFLOP/s": round(rflops / med / 1e12, 1),
+                                    "frac_bf16": round(rflops / med / PEAK_BF16, 4), "ms": round(med * 1e3, 3)}
+        mbytes = 5 * (32 * C * 128 * 2 + 32 * C * 4)
+        med_m, _ = timer.run(lambda: F.lse_merge([b[0] for b in blocks], [b[1] for b in blocks]), reps=20,
+                             flush=flush)
+        extras["ring_c4_merge"] = {"GB/s": round(mbytes / med_m / 1e9, 1),
+                                   "frac_hbm": round(mbytes / med_m / PEAK_HBM, 4), "us": round(med_m * 1e6, 1)}
+        log(f"C4 ring: blocks {med * 1e3:.3f} ms ({rflops / med / 1e12:.0f} TFLOP/s), merge {med_m * 1e6:.1f} us "
+            f"({mbytes / med_m / 1e9:.0f} GB/s)")
+        del q4, k4, v4, blocks
+
+        # C5 MMDiT joint attention, bf16 and fp8
+        q5, k5, v5 = (torch.randn(1, 24, 4608, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+        f5 = 4 * 24 * 128 * 4608 * 4608
+        med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5), reps=10)
+        extras["mmdit_c5a_bf16"] = {"TFLOP/s": round(f5 / med / 1e12, 1), "frac_bf16": round(f5 / med / PEAK_BF16, 4),
+                                    "us": round(med * 1e6, 1)}
+        opt = F.SdpaOption(sage_attn_type="native_fp8")
+        med8, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5, sdpa_option=opt), reps=10)
+        med_q, _ = timer.run(lambda: [F.quantize_fp8_per_head(x) for x in (q5, k5, v5)], reps=10)
+        kern8 = max(med8 - med_q, 1e-9)
+        extras["mmdit_c5b_fp8"] = {"TFLOP/s_end_to_end": round(f5 / med8 / 1e12, 1),
+                                   "TFLOP/s_attention_kernel": round(f5 / kern8 / 1e12, 1),
+                                   "frac_fp8_kernel": round(f5 / kern8 / PEAK_FP8, 4),
+                                   "quantize_us": round(med_q * 1e6, 1), "us": round(med8 * 1e6, 1)}
+        log(f"C5 MMDiT: bf16 {f5 / med / 1e12:.0f} TFLOP/s; fp8 end-to-end {f5 / med8 / 1e12:.0f} TFLOP/s "
+            f"(quantize {med_q * 1e6:.0f} us, attention ~{f5 / kern8 / 1e12:.0f} TFLOP/s)")
+        del q5, k5, v5
+
+        # C1 fp32-spec causal MHA (runs in bf16 on the GPU)
+        q1, k1, v1 = (torch.randn(1, 8, 512, 64, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+        f1 = causal_flops(1, 8, 512, 64)
+        med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q1, k1, v1, is_causal=True), reps=20)
+        extras["c1_causal_mha_d64"] = {"TFLOP/s": round(f1 / med / 1e12, 2), "us": round(med * 1e6, 1)}
+        del flush_buf
+    result["extras"] = extras
+
+    # ---------------------------------------------------------------- CPU baseline (libtorch CPU SDPA)
+    if not args.no_cpu:
+        from oracle import dtorch_cpu_path as cpu
+
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        o_gpu = out[0]
+        # bounded sample: batch 0, the first `nh` query heads (kv heads follow), all 2048 rows
+        def cpu_run(nh):
+            nkv = max(1, nh // (Hq // Hkv))
+            tq = torch.from_numpy(qn[:1, :nh]).to(torch.bfloat16).float()
+            tk = torch.from_numpy(kn[:1, :nkv]).to(torch.bfloat16).float()
+            tv = torch.from_numpy(vn[:1, :nkv]).to(torch.bfloat16).float()
+            t0 = time.perf_counter()
+            r = cpu.sdpa(tq, tk, tv, is_causal=True, enable_gqa=True)
+            return time.perf_counter() - t0, r
+
+        dt1, _ = cpu_run(4)  # warmup + estimate
+        per_head = dt1 / 4
+        nh = int(min(Hq, max(4, (5.0 / max(per_head, 1e-6)) // 4 * 4)))
+        times = []
+        ref = None
+        for _ in range(3):
+            dt, ref = cpu_run(nh)
+            times.append(dt)
+        dt = float(np.median(times))
+        sflops = causal_flops(1, nh, S, D)
+        err = float((o_gpu[:1, :nh].float().cpu() - ref).abs().max())
+        result["cpu_baseline"] = {
+            "value": round(sflops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+            "sample": f"libtorch CPU SDPA fp32 (SdpaOp::Compute's call on a CPU mesh) on batch 0, {nh} of 32 query "
+                      f"heads, S=2048, causal, GQA; median of 3 reps, {dt:.2f} s each; physical cores "
+                      f"{_physical_cores()}, logical CPUs {os.cpu_count()}",
+            "gpu_vs_cpu_max_abs_err": round(err, 5),
+        }
+        log(f"CPU baseline: {sflops / dt / 1e12:.3f} TFLOP/s on {threads} threads ({nh} heads, {dt:.2f} s); "
+            f"GPU vs CPU max-abs {err:.2e}")
+
+    print(json.dumps(result), flush=True)
+
+
+def _physical_cores():
+    try:
+        ids = set()
+        with open("/proc/cpuinfo") as f:
+            phys = core = None
+            for line in f:
+                if line.startswith("physical id"):
+                    phys = line.split(":")[1].strip()
+                elif line.startswith("core id"):
+                    core = line.split(":")[1].strip()
+                    ids.add((phys, core))
+        return len(ids) or None
+    except OSError:
+        return None
+
+
+if __name__ == "__main__":
+    main()

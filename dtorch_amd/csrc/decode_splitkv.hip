@@ -1,0 +1,328 @@
+// Split-KV single-token decode for gfx950.
+//
+// Semantics: for each sequence b, O_b = softmax(scale * q_b K_b[:L_b]^T) V_b[:L_b] with GQA
+// (query head h reads kv head h / (Hq/Hkv)); i.e. SdpaOp::Compute's arithmetic
+// (dtorch/core/operators/standard/scaled_dot_product_attention_op.cc:107-109) at Lq = 1,
+// is_causal = False, over the true length.  The reference has no KV cache or decode op.
+//
+// Kernel 1 (decode_partial_kernel): one workgroup per (b, kv head, chunk of C tokens, head subgroup).
+//   The G query heads of the subgroup share every K/V byte read.  A token row (D * 2 bytes) is read
+//   by D/8 lanes with 16-byte loads, so each load instruction covers whole rows (fully coalesced).
+//   Scores use v_dot2_f32_{bf16,f16} and a butterfly over the D/8 lanes of the row; the chunk's
+//   softmax runs in LDS; P V accumulates in fp32 registers and is reduced across lanes and waves.
+//   Output: a partial O (normalised by its own sum) and a partial LSE per (b, head, chunk).
+//   Chunks past L_b exit immediately; rows at or past L_b are never read.
+// Kernel 2 (decode_merge_kernel): one wave per (b, query head) merges the ceil(L_b / C) partials by
+//   LSE and writes O in the input dtype plus the fp32 LSE.
+#include "dtattn_common.hpp"
+
+namespace dtattn {
+
+struct DecodeParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const int32_t* lengths;
+    void* o;
+    float* lse;
+    float* part_o;    // [B, Hq, nsplit, D]
+    float* part_lse;  // [B, Hq, nsplit]
+    int64_t qs_b, qs_h;
+    int64_t ks_b, ks_h, ks_s;
+    int64_t vs_b, vs_h, vs_s;
+    int64_t os_b, os_h;
+    int64_t lses_b;
+    int32_t B, Hq, Hkv, S_max, group, sub;  // sub = heads handled per workgroup
+    int32_t chunk, nsplit;
+    float c;  // scale * log2(e)
+};
+
+constexpr int kDecodeChunk = 256;
+constexpr int kMaxChunk = 512;
+
+size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk, int64_t* nsplit_out) {
+    const int64_t nsplit = (S_max + chunk - 1) / chunk;
+    if (nsplit_out) *nsplit_out = nsplit;
+    const size_t o_bytes = (size_t)B * Hq * nsplit * D * sizeof(float);
+    const size_t lse_bytes = (size_t)B * Hq * nsplit * sizeof(float);
+    return ((o_bytes + 255) & ~(size_t)255) + ((lse_bytes + 255) & ~(size_t)255);
+}
+
+// G heads per workgroup, D head dim, C tokens per chunk (4 waves x C/4 tokens).
+template <typename T, int D, int G>
+__global__ void __launch_bounds__(256) decode_partial_kernel(const DecodeParams p) {
+    constexpr int LPT = D / 8;          // lanes per token row
+    constexpr int TPI = 64 / LPT;       // tokens per wave-wide load
+    __shared__ float sc[G][kMaxChunk];  // scores, then probabilities
+    __shared__ float red[4][G][D];      // per-wave partial P V
+    __shared__ float stat[G][2];        // max (log2 domain), sum
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int split = blockIdx.x;
+    const int hk = blockIdx.y % p.Hkv;
+    const int sg = blockIdx.y / p.Hkv;   // head subgroup within the kv group
+    const int b = blockIdx.z;
+    const int L = min(max(p.lengths[b], 0), p.S_max);  // never read past the cache
+    const int C = p.chunk;
+    const int t0 = split * C;
+    if (t0 >= L) return;
+    const int n_tok = min(C, L - t0);
+    const int tpw = C / 4;               // tokens per wave
+    const int NI = tpw / TPI;            // loads per wave
+
+    const int hq0 = hk * p.group + sg * G;
+    const int c8 = lane % LPT;           // 16-byte chunk of the row this lane reads
+    const int tsub = lane / LPT;
+
+    // q chunks for the G heads (packed pairs for v_dot2).
+    u32x4 qv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        qv[g] = ld16(reinterpret_cast<const T*>(p.q) + b * p.qs_b + (hq0 + g) * p.qs_h + c8 * 8);
+
+    const T* kp = reinterpret_cast<const T*>(p.k) + b * p.ks_b + hk * p.ks_h;
+    const T* vp = reinterpret_cast<const T*>(p.v) + b * p.vs_b + hk * p.vs_h;
+
+    // ---- scores
+    for (int i0 = 0; i0 < NI; i0 += 8) {
+        u32x4 kr[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int tl = wave * tpw + (i0 + j) * TPI + tsub;
+            kr[j] = u32x4{0u, 0u, 0u, 0u};
+            if (i0 + j < NI && tl < n_tok) kr[j] = ld16(kp + (int64_t)(t0 + tl) * p.ks_s + c8 * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (i0 + j >= NI) break;
+            const int tl = wave * tpw + (i0 + j) * TPI + tsub;
+            float sg_[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float acc = 0.f;
+                acc = Elem<T>::dot2(kr[j].x, qv[g].x, acc);
+                acc = Elem<T>::dot2(kr[j].y, qv[g].y, acc);
+                acc = Elem<T>::dot2(kr[j].z, qv[g].z, acc);
+                acc = Elem<T>::dot2(kr[j].w, qv[g].w, acc);
+#pragma unroll
+                for (int m = 1; m < LPT; m <<= 1) acc += shfl_xor_f(acc, m);
+                sg_[g] = acc;
+            }
+            if (c8 == 0 && tl < C) {
+#pragma unroll
+                for (int g = 0; g < G; ++g) sc[g][tl] = tl < n_tok ? sg_[g] * p.c : kNegInf;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- softmax over the chunk (log2 domain), one wave per head (round robin)
+    for (int g = wave; g < G; g += 4) {
+        float mx = kNegInf;
+        for (int t = lane; t < C; t += 64) mx = fmaxf(mx, sc[g][t]);
+        mx = wave_max(mx);
+        float sum = 0.f;
+        for (int t = lane; t < C; t += 64) {
+            const float e = fast_exp2(sc[g][t] - mx);
+            sc[g][t] = e;
+            sum += e;
+        }
+        sum = wave_sum(sum);
+        if (lane == 0) {
+            stat[g][0] = mx;
+            stat[g][1] = sum;
+        }
+    }
+    __syncthreads();
+
+    // ---- P V
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+    for (int i0 = 0; i0 < NI; i0 += 8) {
+        u32x4 vr[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int tl = wave * tpw + (i0 + j) * TPI + tsub;
+            vr[j] = u32x4{0u, 0u, 0u, 0u};
+            if (i0 + j < NI && tl < n_tok) vr[j] = ld16(vp + (int64_t)(t0 + tl) * p.vs_s + c8 * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (i0 + j >= NI) break;
+            const int tl = wave * tpw + (i0 + j) * TPI + tsub;
+            if (tl >= n_tok) continue;
+            float vf[8];
+            unpack8<T>(vr[j], vf);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float pw = sc[g][tl];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] = __builtin_fmaf(pw, vf[e], acc[g][e]);
+            }
+        }
+    }
+    // reduce across the TPI token lanes that share a chunk, then across waves through LDS
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float x = acc[g][e];
+#pragma unroll
+            for (int m = LPT; m < 64; m <<= 1) x += shfl_xor_f(x, m);
+            acc[g][e] = x;
+        }
+    if (tsub == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) red[wave][g][c8 * 8 + e] = acc[g][e];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * D; idx += 256) {
+        const int g = idx / D, d = idx % D;
+        const float sum = stat[g][1];
+        const float val = (red[0][g][d] + red[1][g][d] + red[2][g][d] + red[3][g][d]) / sum;
+        const int hq = hq0 + g;
+        p.part_o[(((int64_t)b * p.Hq + hq) * p.nsplit + split) * D + d] = val;
+        if (d == 0) p.part_lse[((int64_t)b * p.Hq + hq) * p.nsplit + split] = (stat[g][0] + __log2f(sum)) * kLn2;
+    }
+}
+
+// One wave per (b, query head).
+template <typename T, int D>
+__global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p) {
+    constexpr int DPL = D / 64;  // d values per lane
+    const int lane = threadIdx.x & 63;
+    const int64_t pair = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (pair >= (int64_t)p.B * p.Hq) return;
+    const int b = (int)(pair / p.Hq), hq = (int)(pair % p.Hq);
+    const int L = min(max(p.lengths[b], 0), p.S_max);
+    const int ns = (L + p.chunk - 1) / p.chunk;
+    T* op = reinterpret_cast<T*>(p.o) + b * p.os_b + hq * p.os_h;
+    if (ns == 0) {  // empty sequence: O = 0, LSE = -inf
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) op[lane * DPL + e] = Elem<T>::from_f32(0.f);
+        if (p.lse != nullptr && lane == 0) p.lse[b * p.lses_b + hq] = kNegInf;
+        return;
+    }
+    const float* pl = p.part_lse + pair * p.nsplit;
+    const float* po = p.part_o + pair * p.nsplit * D;
+
+    float mx = kNegInf;
+    for (int s = lane; s < ns; s += 64) mx = fmaxf(mx, pl[s]);
+    mx = wave_max(mx);
+    float sum = 0.f;
+    for (int s = lane; s < ns; s += 64) sum += __expf(pl[s] - mx);
+    sum = wave_sum(sum);
+    float acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+    for (int s = 0; s < ns; ++s) {
+        const float w = __expf(pl[s] - mx) / sum;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(w, po[(int64_t)s * D + lane * DPL + e], acc[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) op[lane * DPL + e] = Elem<T>::from_f32(acc[e]);
+    if (p.lse != nullptr && lane == 0) p.lse[b * p.lses_b + hq] = mx + __logf(sum);
+}
+
+template <typename T, int D, int G>
+static int launch_decode(const DecodeParams& p, hipStream_t stream) {
+    dim3 grid1((unsigned)p.nsplit, (unsigned)(p.Hkv * (p.group / G)), (unsigned)p.B);
+    hipLaunchKernelGGL((decode_partial_kernel<T, D, G>), grid1, dim3(256), 0, stream, p);
+    int st = check_launch("decode_partial_kernel");
+    if (st != DTATTN_OK) return st;
+    const int64_t pairs = (int64_t)p.B * p.Hq;
+    hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, stream, p);
+    return check_launch("decode_merge_kernel");
+}
+
+template <typename T, int D>
+static int dispatch_group(const DecodeParams& p, hipStream_t stream) {
+    const int g = p.group;
+    if (g % 8 == 0) return launch_decode<T, D, 8>(p, stream);
+    if (g % 4 == 0) return launch_decode<T, D, 4>(p, stream);
+    if (g % 2 == 0) return launch_decode<T, D, 2>(p, stream);
+    return launch_decode<T, D, 1>(p, stream);
+}
+
+template <typename T>
+static int dispatch_decode(const DecodeParams& p, int D, hipStream_t stream) {
+    if (D == 128) return dispatch_group<T, 128>(p, stream);
+    if (D == 64) return dispatch_group<T, 64>(p, stream);
+    return fail(DTATTN_ERR_UNSUPPORTED, "decode: head dim %d not supported (64 or 128)", D);
+}
+
+}  // namespace dtattn
+
+using namespace dtattn;
+
+extern "C" size_t dtattn_decode_workspace_size(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk) {
+    if (chunk <= 0) chunk = kDecodeChunk;
+    if (B <= 0 || Hq <= 0 || S_max <= 0 || D <= 0) return 0;
+    return decode_ws_parts(B, Hq, S_max, D, chunk, nullptr);
+}
+
+extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_) {
+    if (a == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: args is NULL");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (a->B < 0 || a->Hq <= 0 || a->Hkv <= 0 || a->S_max <= 0 || a->D <= 0)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: bad sizes");
+    if (a->Hq % a->Hkv != 0) return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: Hq is not a multiple of Hkv");
+    if (a->B == 0) return DTATTN_OK;
+    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16)
+        return fail(DTATTN_ERR_UNSUPPORTED, "decode: dtype %d not supported (bf16, fp16)", a->dtype);
+    const int32_t chunk = a->chunk > 0 ? a->chunk : kDecodeChunk;
+    if (chunk % 64 != 0 || chunk > kMaxChunk)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: chunk %d must be a multiple of 64 and <= %d", chunk,
+                    kMaxChunk);
+    if (a->q == nullptr || a->k_cache == nullptr || a->v_cache == nullptr || a->lengths == nullptr || a->o == nullptr)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: null pointer");
+    const int64_t esz = 2;
+    const int64_t s_all[] = {a->q_stride[0], a->q_stride[1], a->k_stride[0], a->k_stride[1], a->k_stride[2],
+                             a->v_stride[0], a->v_stride[1], a->v_stride[2]};
+    for (int64_t s : s_all)
+        if ((s * esz) % 16 != 0) return fail(DTATTN_ERR_UNSUPPORTED, "decode: strides must be multiples of 16 bytes");
+    int64_t nsplit = 0;
+    const size_t need = decode_ws_parts(a->B, a->Hq, a->S_max, a->D, chunk, &nsplit);
+    if (a->workspace == nullptr || a->workspace_bytes < need)
+        return fail(DTATTN_ERR_WORKSPACE, "decode: workspace of %zu bytes required, %zu given", need,
+                    a->workspace_bytes);
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
+        return fail(DTATTN_ERR_WORKSPACE, "decode: workspace must be 256-byte aligned");
+    if (nsplit > 65535 || a->B > 65535) return fail(DTATTN_ERR_UNSUPPORTED, "decode: grid too large");
+
+    DecodeParams p;
+    p.q = a->q;
+    p.k = a->k_cache;
+    p.v = a->v_cache;
+    p.lengths = a->lengths;
+    p.o = a->o;
+    p.lse = a->lse;
+    const size_t o_bytes = (size_t)a->B * a->Hq * nsplit * a->D * sizeof(float);
+    p.part_o = reinterpret_cast<float*>(a->workspace);
+    p.part_lse = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + ((o_bytes + 255) & ~(size_t)255));
+    p.qs_b = a->q_stride[0], p.qs_h = a->q_stride[1];
+    p.ks_b = a->k_stride[0], p.ks_h = a->k_stride[1], p.ks_s = a->k_stride[2];
+    p.vs_b = a->v_stride[0], p.vs_h = a->v_stride[1], p.vs_s = a->v_stride[2];
+    p.os_b = a->o_stride[0], p.os_h = a->o_stride[1];
+    p.lses_b = a->lse ? a->lse_stride[0] : 0;
+    p.B = (int32_t)a->B;
+    p.Hq = (int32_t)a->Hq;
+    p.Hkv = (int32_t)a->Hkv;
+    p.S_max = (int32_t)a->S_max;
+    p.group = (int32_t)(a->Hq / a->Hkv);
+    p.sub = 0;
+    p.chunk = chunk;
+    p.nsplit = (int32_t)nsplit;
+    const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
+    p.c = scale * kLog2e;
+    if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t>(p, (int)a->D, stream);
+    return dispatch_decode<f16_t>(p, (int)a->D, stream);
+}

@@ -1,0 +1,112 @@
+// Shared device helpers for the gfx950 attention kernels: vector types, bf16/fp16/fp8 conversions,
+// MFMA wrappers and the launch-side argument checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dtattn.h"
+
+namespace dtattn {
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+typedef bf16_t bf16x8 __attribute__((ext_vector_type(8)));
+typedef bf16_t bf16x4 __attribute__((ext_vector_type(4)));
+typedef bf16_t bf16x2 __attribute__((ext_vector_type(2)));
+typedef f16_t f16x8 __attribute__((ext_vector_type(8)));
+typedef f16_t f16x4 __attribute__((ext_vector_type(4)));
+typedef f16_t f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+// ---- element traits -------------------------------------------------------------------------
+
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<bf16_t> {
+    typedef bf16x8 vec8;
+    typedef bf16x4 vec4;
+    static __device__ __forceinline__ float to_f32(bf16_t x) { return static_cast<float>(x); }
+    static __device__ __forceinline__ bf16_t from_f32(float x) { return static_cast<bf16_t>(x); }
+    static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                               false);
+    }
+};
+
+template <>
+struct Elem<f16_t> {
+    typedef f16x8 vec8;
+    typedef f16x4 vec4;
+    static __device__ __forceinline__ float to_f32(f16_t x) { return static_cast<float>(x); }
+    static __device__ __forceinline__ f16_t from_f32(float x) { return static_cast<f16_t>(x); }
+    static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+    }
+};
+
+// Unpack a 16-byte chunk of 8 elements into fp32.
+template <typename T>
+__device__ __forceinline__ void unpack8(u32x4 raw, float* out) {
+    typedef typename Elem<T>::vec8 V;
+    V v = __builtin_bit_cast(V, raw);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = Elem<T>::to_f32(v[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ u32x4 pack8(const float* in) {
+    typedef typename Elem<T>::vec8 V;
+    V v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = Elem<T>::from_f32(in[i]);
+    return __builtin_bit_cast(u32x4, v);
+}
+
+// ---- raw memory access ------------------------------------------------------------------------
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// ---- wave helpers -----------------------------------------------------------------------------
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_f(v, m);
+    return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---- host-side status plumbing ----------------------------------------------------------------
+
+void set_last_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+}  // namespace dtattn

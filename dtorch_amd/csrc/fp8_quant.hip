@@ -1,0 +1,155 @@
+// Per-head absmax quantization to OCP fp8 e4m3fn (pre-pass of the fp8 prefill).
+//
+// Supersedes the quantization inside the reference's SageAttention branch
+// (dtorch/external/sage_attn/sage_attn_adapter.cc:28-158).  For each (b, h):
+//   amax = max|x|, inv = 448 / amax, code = e4m3fn_rne(float(x * inv)) saturated to +-448,
+//   descale = amax / 448 (amax == 0: inv = descale = 1).
+// Two launches, no atomics and no zero-initialised memory:
+//   1. fp8_absmax_partial_kernel: one workgroup per (b, h, slice of rows) writes the slice's max|x|.
+//   2. fp8_quantize_kernel: each workgroup reduces its head's slice maxima, then converts its slice
+//      with v_cvt_pk_fp8_f32 (round to nearest even) and writes 16 codes per thread per step.
+#include "dtattn_common.hpp"
+
+namespace dtattn {
+
+constexpr int kQuantRowsPerSlice = 256;
+
+struct QuantParams {
+    const void* x;
+    uint8_t* x8;
+    float* descale;
+    float* part;  // [B*H, nslice]
+    int64_t xs_b, xs_h, xs_s;
+    int32_t B, H, S, D, nslice;
+};
+
+template <typename T>
+__device__ __forceinline__ void load_row8(const T* p, float* out) {
+    unpack8<T>(ld16(p), out);
+}
+template <>
+__device__ __forceinline__ void load_row8<float>(const float* p, float* out) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+    out[0] = a.x, out[1] = a.y, out[2] = a.z, out[3] = a.w;
+    out[4] = b.x, out[5] = b.y, out[6] = b.z, out[7] = b.w;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) fp8_absmax_partial_kernel(const QuantParams p) {
+    __shared__ float wmax[4];
+    const int slice = blockIdx.x;
+    const int bh = blockIdx.y;
+    const int b = bh / p.H, h = bh % p.H;
+    const T* xp = reinterpret_cast<const T*>(p.x) + b * p.xs_b + h * p.xs_h;
+    const int cpr = p.D / 8;
+    const int r0 = slice * kQuantRowsPerSlice;
+    const int r1 = min(p.S, r0 + kQuantRowsPerSlice);
+    float m = 0.f;
+    for (int idx = threadIdx.x; idx < (r1 - r0) * cpr; idx += 256) {
+        const int r = r0 + idx / cpr, c = idx % cpr;
+        float v[8];
+        load_row8<T>(xp + (int64_t)r * p.xs_s + c * 8, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+    }
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        p.part[(int64_t)bh * p.nslice + slice] = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) fp8_quantize_kernel(const QuantParams p) {
+    __shared__ float s_inv;
+    const int slice = blockIdx.x;
+    const int bh = blockIdx.y;
+    const int b = bh / p.H, h = bh % p.H;
+    if (threadIdx.x < 64) {
+        float m = 0.f;
+        for (int i = threadIdx.x; i < p.nslice; i += 64) m = fmaxf(m, p.part[(int64_t)bh * p.nslice + i]);
+        m = wave_max(m);
+        if (threadIdx.x == 0) {
+            const float inv = m > 0.f ? 448.f / m : 1.f;
+            s_inv = inv;
+            if (slice == 0) p.descale[bh] = m > 0.f ? m / 448.f : 1.f;
+        }
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    const T* xp = reinterpret_cast<const T*>(p.x) + b * p.xs_b + h * p.xs_h;
+    uint8_t* yp = p.x8 + ((int64_t)bh * p.S) * p.D;
+    const int cpr = p.D / 16;  // 16 codes per thread per step
+    const int r0 = slice * kQuantRowsPerSlice;
+    const int r1 = min(p.S, r0 + kQuantRowsPerSlice);
+    for (int idx = threadIdx.x; idx < (r1 - r0) * cpr; idx += 256) {
+        const int r = r0 + idx / cpr, c = idx % cpr;
+        float v[16];
+        load_row8<T>(xp + (int64_t)r * p.xs_s + c * 16, v);
+        load_row8<T>(xp + (int64_t)r * p.xs_s + c * 16 + 8, v + 8);
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = fminf(fmaxf(v[4 * k + e] * inv, -448.f), 448.f);
+            int packed = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+            packed = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], packed, true);
+            w[k] = (uint32_t)packed;
+        }
+        st16(yp + (int64_t)r * p.D + c * 16, u32x4{w[0], w[1], w[2], w[3]});
+    }
+}
+
+template <typename T>
+static int launch_quant(const QuantParams& p, hipStream_t stream) {
+    dim3 grid((unsigned)p.nslice, (unsigned)(p.B * p.H));
+    hipLaunchKernelGGL((fp8_absmax_partial_kernel<T>), grid, dim3(256), 0, stream, p);
+    int st = check_launch("fp8_absmax_partial_kernel");
+    if (st != DTATTN_OK) return st;
+    hipLaunchKernelGGL((fp8_quantize_kernel<T>), grid, dim3(256), 0, stream, p);
+    return check_launch("fp8_quantize_kernel");
+}
+
+}  // namespace dtattn
+
+using namespace dtattn;
+
+extern "C" size_t dtattn_fp8_quantize_workspace_size(int64_t B, int64_t H, int64_t S, int64_t D) {
+    (void)D;
+    if (B <= 0 || H <= 0 || S <= 0) return 0;
+    const int64_t nslice = (S + kQuantRowsPerSlice - 1) / kQuantRowsPerSlice;
+    return (((size_t)B * H * nslice * sizeof(float)) + 255) & ~(size_t)255;
+}
+
+extern "C" int dtattn_fp8_quantize_per_head(const void* x, int32_t x_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                                            const int64_t x_stride[3], void* x8, float* descale, void* workspace,
+                                            size_t workspace_bytes, void* stream_) {
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (B < 0 || H < 0 || S < 0 || D <= 0) return fail(DTATTN_ERR_INVALID_ARGUMENT, "quantize: bad sizes");
+    if (D % 16 != 0) return fail(DTATTN_ERR_UNSUPPORTED, "quantize: D=%lld must be a multiple of 16", (long long)D);
+    if (B == 0 || H == 0 || S == 0) return DTATTN_OK;
+    if (x == nullptr || x8 == nullptr || descale == nullptr || x_stride == nullptr)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "quantize: null pointer");
+    if (B * H > 65535 || S > 0x3fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "quantize: sizes too large");
+    const int esz = x_dtype == DTATTN_FP32 ? 4 : 2;
+    for (int j = 0; j < 3; ++j)
+        if ((x_stride[j] * esz) % 16 != 0)
+            return fail(DTATTN_ERR_UNSUPPORTED, "quantize: strides must be multiples of 16 bytes");
+    const size_t need = dtattn_fp8_quantize_workspace_size(B, H, S, D);
+    if (workspace == nullptr || workspace_bytes < need)
+        return fail(DTATTN_ERR_WORKSPACE, "quantize: workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    QuantParams p;
+    p.x = x;
+    p.x8 = reinterpret_cast<uint8_t*>(x8);
+    p.descale = descale;
+    p.part = reinterpret_cast<float*>(workspace);
+    p.xs_b = x_stride[0], p.xs_h = x_stride[1], p.xs_s = x_stride[2];
+    p.B = (int32_t)B, p.H = (int32_t)H, p.S = (int32_t)S, p.D = (int32_t)D;
+    p.nslice = (int32_t)((S + kQuantRowsPerSlice - 1) / kQuantRowsPerSlice);
+    if (x_dtype == DTATTN_BF16) return launch_quant<bf16_t>(p, stream);
+    if (x_dtype == DTATTN_FP16) return launch_quant<f16_t>(p, stream);
+    if (x_dtype == DTATTN_FP32) return launch_quant<float>(p, stream);
+    return fail(DTATTN_ERR_UNSUPPORTED, "quantize: dtype %d not supported", x_dtype);
+}

@@ -1,0 +1,419 @@
+// Host operators of the MI355X attention path (see sdpa_op.h).  All arithmetic goes through the
+// dtattn C ABI; this file only validates, allocates outputs/workspace from the c10 caching
+// allocator on the current device, and launches on the thread's current HIP stream (the stream the
+// reference's KernelStream thread sets once: dtorch/core/kernel_stream/cuda_kernel_stream.cc:25-43).
+// It never creates or switches streams and never synchronises.
+#include "sdpa_op.h"
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <cmath>
+#include <sstream>
+#include <stdexcept>
+
+#include "dtattn.h"
+
+namespace dtorch_amd {
+namespace core {
+
+namespace {
+
+[[noreturn]] void Throw(const std::string& msg) { throw std::invalid_argument("dtorch_amd: " + msg); }
+
+void Check(int status, const char* what) {
+    if (status == DTATTN_OK) return;
+    std::ostringstream os;
+    os << what << " failed (status " << status << "): " << dtattn_last_error();
+    if (status == DTATTN_ERR_LAUNCH || status == DTATTN_ERR_DEVICE) throw std::runtime_error("dtorch_amd: " + os.str());
+    Throw(os.str());
+}
+
+void* CurrentStream(const at::Tensor& t) {
+    return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+int32_t DtypeCode(c10::ScalarType st) {
+    switch (st) {
+        case c10::ScalarType::BFloat16: return DTATTN_BF16;
+        case c10::ScalarType::Half: return DTATTN_FP16;
+        case c10::ScalarType::Float8_e4m3fn: return DTATTN_FP8_E4M3FN;
+        case c10::ScalarType::Float: return DTATTN_FP32;
+        default: return -1;
+    }
+}
+
+// A tensor viewed as [B, H, S, D] (leading axes folded into B), last-axis stride 1, 16-byte aligned
+// strides and base pointer.  Anything else is made contiguous first (a layout copy, not compute).
+struct View4 {
+    at::Tensor t;
+    int64_t B, H, S, D;
+    int64_t sb, sh, ss;
+};
+
+bool Foldable(const at::Tensor& t) {
+    const int64_t nd = t.dim();
+    for (int64_t i = 0; i + 1 <= nd - 4; ++i) {
+        if (t.size(i + 1) != 1 && t.stride(i) != t.stride(i + 1) * t.size(i + 1)) return false;
+    }
+    return true;
+}
+
+View4 MakeView4(const at::Tensor& in, const char* name) {
+    if (in.dim() < 4) Throw(std::string(name) + " must have at least 4 dimensions [..., H, S, D]");
+    at::Tensor t = in;
+    const int64_t esz = t.element_size();
+    auto ok = [&](const at::Tensor& x) {
+        if (x.stride(-1) != 1 || !Foldable(x)) return false;
+        if ((reinterpret_cast<uintptr_t>(x.data_ptr()) & 15u) != 0) return false;
+        for (int64_t i = 0; i < x.dim() - 1; ++i)
+            if (x.size(i) > 1 && (x.stride(i) * esz) % 16 != 0) return false;
+        return true;
+    };
+    if (!ok(t)) t = t.contiguous();
+    View4 v;
+    v.t = t;
+    const int64_t nd = t.dim();
+    v.B = 1;
+    for (int64_t i = 0; i < nd - 3; ++i) v.B *= t.size(i);
+    v.H = t.size(nd - 3);
+    v.S = t.size(nd - 2);
+    v.D = t.size(nd - 1);
+    v.sb = nd > 3 ? t.stride(nd - 4) : 0;
+    if (nd > 3 && t.size(nd - 4) == 1) v.sb = v.H * t.stride(nd - 3);
+    v.sh = t.stride(nd - 3);
+    v.ss = t.stride(nd - 2);
+    if (v.H == 1) v.sh = v.S * v.ss;
+    return v;
+}
+
+void CheckDevice(const std::vector<const at::Tensor*>& ts) {
+    const at::Device dev = ts[0]->device();
+    if (!dev.is_cuda())
+        Throw("the MI355X attention kernels take device tensors; CPU meshes keep DTorch's libtorch path");
+    for (const at::Tensor* t : ts)
+        if (t->device() != dev) Throw("all tensors must be on the same device");
+}
+
+struct PrefillResult {
+    at::Tensor o, lse;
+};
+
+PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_, const SdpaParam& prm,
+                         int64_t qOffset, int64_t kOffset, bool wantLse) {
+    CheckDevice({&q_, &k_, &v_});
+    c10::DeviceGuard guard(q_.device());
+    if (q_.dim() != k_.dim() || q_.dim() != v_.dim()) Throw("query, key and value must have the same rank");
+    for (int64_t i = 0; i < q_.dim() - 3; ++i)
+        if (q_.size(i) != k_.size(i) || q_.size(i) != v_.size(i))
+            Throw("query, key and value batch dimensions differ");
+    if (q_.size(-1) != k_.size(-1)) Throw("query and key head dims differ");
+    if (k_.size(-2) != v_.size(-2) || k_.size(-3) != v_.size(-3)) Throw("key and value shapes differ");
+    const int64_t hq = q_.size(-3), hkv = k_.size(-3);
+    if (hq != hkv) {
+        if (!prm.enableGqa) Throw("query and key/value head counts differ; set enable_gqa=True");
+        if (hq % hkv != 0) Throw("number of query heads must be a multiple of key/value heads");
+    }
+    if (prm.scale.has_value() && !(prm.scale.value() > 0.0)) Throw("scale must be positive");
+
+    std::string quant;
+    if (prm.option.has_value()) quant = prm.option->sageAttentionType;
+    const bool fp8 = quant == "native_fp8";
+    if (!quant.empty() && !fp8)
+        Throw("sage_attn_type '" + quant +
+              "' selects the third-party SageAttention package, which this build does not ship; use '' or "
+              "'native_fp8'");
+
+    const c10::ScalarType st = q_.scalar_type();
+    if (k_.scalar_type() != st || v_.scalar_type() != st) Throw("query, key and value dtypes differ");
+    if (st != c10::ScalarType::BFloat16 && st != c10::ScalarType::Half)
+        Throw(std::string("dtype ") + c10::toString(st) + " is not supported by the MI355X kernels (bf16, fp16)");
+    if (fp8 && st != c10::ScalarType::BFloat16) Throw("native_fp8 takes bf16 inputs");
+
+    std::vector<int64_t> oshape = q_.sizes().vec();
+    oshape.back() = v_.size(-1);
+    at::Tensor o = at::empty(oshape, q_.options());
+    std::vector<int64_t> lshape(q_.sizes().begin(), q_.sizes().end() - 1);
+    at::Tensor lse = wantLse ? at::empty(lshape, q_.options().dtype(at::kFloat)) : at::Tensor();
+    if (o.numel() == 0) return {o, lse};
+
+    View4 q = MakeView4(q_, "query"), k = MakeView4(k_, "key"), v = MakeView4(v_, "value");
+    View4 ov = MakeView4(o, "output");
+    void* stream = CurrentStream(q_);
+
+    dtattn_prefill_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.B = q.B, a.Hq = q.H, a.Hkv = k.H, a.Sq = q.S, a.Sk = k.S, a.D = q.D, a.Dv = v.D;
+    a.o = ov.t.data_ptr();
+    a.o_stride[0] = ov.sb, a.o_stride[1] = ov.sh, a.o_stride[2] = ov.ss;
+    if (wantLse) {
+        a.lse = lse.data_ptr<float>();
+        a.lse_stride[0] = q.H * q.S, a.lse_stride[1] = q.S;
+    }
+    a.scale = prm.scale.has_value() ? (float)prm.scale.value() : 0.f;
+    a.causal = prm.isCausal ? 1 : 0;
+    a.q_offset = qOffset, a.k_offset = kOffset;
+
+    at::Tensor q8, k8, v8, qd, kd, vd;
+    if (fp8) {
+        auto quantize = [&](const View4& x, at::Tensor& codes, at::Tensor& desc) {
+            codes = at::empty({x.B, x.H, x.S, x.D}, x.t.options().dtype(at::kFloat8_e4m3fn));
+            desc = at::empty({x.B, x.H}, x.t.options().dtype(at::kFloat));
+            const size_t ws = dtattn_fp8_quantize_workspace_size(x.B, x.H, x.S, x.D);
+            at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, x.t.options().dtype(at::kByte));
+            const int64_t strides[3] = {x.sb, x.sh, x.ss};
+            Check(dtattn_fp8_quantize_per_head(x.t.data_ptr(), DtypeCode(st), x.B, x.H, x.S, x.D, strides,
+                                               codes.data_ptr(), desc.data_ptr<float>(), wst.data_ptr(), ws, stream),
+                  "dtattn_fp8_quantize_per_head");
+        };
+        quantize(q, q8, qd);
+        quantize(k, k8, kd);
+        quantize(v, v8, vd);
+        a.q = q8.data_ptr(), a.k = k8.data_ptr(), a.v = v8.data_ptr();
+        a.q_stride[0] = q.H * q.S * q.D, a.q_stride[1] = q.S * q.D, a.q_stride[2] = q.D;
+        a.k_stride[0] = k.H * k.S * k.D, a.k_stride[1] = k.S * k.D, a.k_stride[2] = k.D;
+        a.v_stride[0] = v.H * v.S * v.D, a.v_stride[1] = v.S * v.D, a.v_stride[2] = v.D;
+        a.dtype = DTATTN_FP8_E4M3FN;
+        a.o_dtype = DTATTN_BF16;
+        a.q_descale = qd.data_ptr<float>(), a.k_descale = kd.data_ptr<float>(), a.v_descale = vd.data_ptr<float>();
+    } else {
+        a.q = q.t.data_ptr(), a.k = k.t.data_ptr(), a.v = v.t.data_ptr();
+        a.q_stride[0] = q.sb, a.q_stride[1] = q.sh, a.q_stride[2] = q.ss;
+        a.k_stride[0] = k.sb, a.k_stride[1] = k.sh, a.k_stride[2] = k.ss;
+        a.v_stride[0] = v.sb, a.v_stride[1] = v.sh, a.v_stride[2] = v.ss;
+        a.dtype = DtypeCode(st);
+        a.o_dtype = a.dtype;
+    }
+    Check(dtattn_prefill_fwd(&a, stream), "dtattn_prefill_fwd");
+    if (!ov.t.is_same(o)) o.copy_(ov.t);
+    return {o, lse};
+}
+
+}  // namespace
+
+Shape SdpaOp::InferOutputMetaInfo(const Shape& q, const Shape& k, const Shape& v) const {
+    if (q.size() < 4 || k.size() < 4 || v.size() < 4) Throw("q, k and v must have at least 4 axes");
+    Shape out = q;
+    out.back() = v.back();
+    return out;
+}
+
+PlacementSignature SdpaOp::GetPlacementSignature(size_t numAxis) const {
+    if (numAxis < 4) Throw("placement signature needs at least 4 axes");
+    PlacementSignature sig;
+    const std::vector<bool> opt = {false, false, false, true};
+    sig.push_back({{"S(0)", "S(0)", "S(0)", "S(0)"}, {"S(0)"}, opt});
+    for (size_t i = 1; i < numAxis - 2; ++i) {
+        const std::string s = "S(" + std::to_string(i) + ")";
+        sig.push_back({{s, s, s, "R"}, {s}, opt});
+    }
+    sig.push_back({{"S(2)", "R", "R", "R"}, {"S(2)"}, opt});
+    sig.push_back({{"R", "R", "R", "R"}, {"R"}, opt});
+    return sig;
+}
+
+std::vector<std::string> SdpaOp::MatchPlacements(size_t numAxis, const std::vector<std::string>& inputs) const {
+    const PlacementSignature sig = GetPlacementSignature(numAxis);
+    for (const PlacementRule& r : sig) {
+        if (inputs.size() != r.inputs.size()) continue;
+        bool match = true;
+        for (size_t i = 0; i < inputs.size() && match; ++i) {
+            if (inputs[i].empty() && r.optional[i]) continue;
+            match = inputs[i] == r.inputs[i];
+        }
+        if (match) return r.outputs;
+    }
+    std::ostringstream os;
+    os << "no placement rule for inputs (";
+    for (size_t i = 0; i < inputs.size(); ++i) os << (i ? ", " : "") << (inputs[i].empty() ? "-" : inputs[i]);
+    os << ")";
+    Throw(os.str());
+}
+
+int64_t SdpaOp::GetOperatorCost(const Shape& q, const Shape& k, const Shape& v) const {
+    if (q.size() < 4) Throw("cost needs at least 4 axes");
+    // batch = Shape::Prod(0, NumAxis - 4), an inclusive range (dtorch/api/cpp/shape.cc:65-75).
+    int64_t batch = 1;
+    for (size_t i = 0; i + 4 <= q.size(); ++i) batch *= q[i];
+    const int64_t qHeads = q[q.size() - 3], seqQ = q[q.size() - 2], headDim = q.back();
+    const int64_t seqKv = k[k.size() - 2], eV = v.back();
+    return 2 * batch * qHeads * seqQ * seqKv * (headDim + eV);
+}
+
+int64_t SdpaOp::GetAlgorithmicFlops(const Shape& q, const Shape& k, const Shape& v) const {
+    int64_t batch = 1;
+    for (size_t i = 0; i + 3 < q.size(); ++i) batch *= q[i];
+    const int64_t qHeads = q[q.size() - 3], L = q[q.size() - 2], D = q.back();
+    const int64_t S = k[k.size() - 2], eV = v.back();
+    int64_t pairs = L * S;
+    if (mParam.isCausal) {
+        pairs = 0;
+        for (int64_t i = 0; i < L; ++i) pairs += std::min<int64_t>(std::max<int64_t>(i + 1, 0), S);
+    }
+    return 2 * (D + eV) * batch * qHeads * pairs;
+}
+
+void SdpaOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
+    if (inputs.size() != 4) Throw("SdpaOp expects 4 inputs {query, key, value, attn_mask}");
+    if (!inputs[0].has_value() || !inputs[1].has_value() || !inputs[2].has_value())
+        Throw("query, key and value are required");
+    if (inputs[3].has_value() && inputs[3]->defined())
+        Throw("attn_mask is not supported by the MI355X kernels (use is_causal)");
+    outputs.push_back(RunPrefill(*inputs[0], *inputs[1], *inputs[2], mParam, 0, 0, false).o);
+}
+
+void SdpaWithLseOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
+    if (inputs.size() != 4) Throw("SdpaWithLseOp expects 4 inputs {query, key, value, attn_mask}");
+    if (!inputs[0].has_value() || !inputs[1].has_value() || !inputs[2].has_value())
+        Throw("query, key and value are required");
+    if (inputs[3].has_value() && inputs[3]->defined())
+        Throw("attn_mask is not supported by the MI355X kernels (use is_causal)");
+    PrefillResult r = RunPrefill(*inputs[0], *inputs[1], *inputs[2], mParam, mQOffset, mKOffset, true);
+    outputs.push_back(r.o);
+    outputs.push_back(r.lse);
+}
+
+void SdpaDecodeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
+    if (inputs.size() != 4 || !inputs[0] || !inputs[1] || !inputs[2] || !inputs[3])
+        Throw("SdpaDecodeOp expects 4 inputs {query, k_cache, v_cache, lengths}");
+    const at::Tensor &q = *inputs[0], &kc = *inputs[1], &vc = *inputs[2], &len = *inputs[3];
+    CheckDevice({&q, &kc, &vc, &len});
+    c10::DeviceGuard guard(q.device());
+    if (q.dim() != 4 || kc.dim() != 4 || vc.dim() != 4) Throw("decode tensors must be 4-D [B, H, S, D]");
+    if (q.size(2) != 1) Throw("decode query must have one token per sequence ([B, Hq, 1, D])");
+    if (kc.sizes() != vc.sizes()) Throw("k_cache and v_cache shapes differ");
+    if (q.size(0) != kc.size(0) || q.size(3) != kc.size(3)) Throw("query and cache shapes do not match");
+    if (q.size(1) % kc.size(1) != 0) Throw("number of query heads must be a multiple of kv heads");
+    if (len.scalar_type() != at::kInt || len.dim() != 1 || len.size(0) != q.size(0))
+        Throw("lengths must be an int32 tensor of shape [B]");
+    const c10::ScalarType st = q.scalar_type();
+    if (kc.scalar_type() != st || vc.scalar_type() != st) Throw("query and cache dtypes differ");
+    if (st != at::kBFloat16 && st != at::kHalf) Throw("decode supports bf16 and fp16");
+    if (mScale.has_value() && !(mScale.value() > 0.0)) Throw("scale must be positive");
+
+    at::Tensor o = at::empty(q.sizes(), q.options());
+    at::Tensor lse = at::empty({q.size(0), q.size(1)}, q.options().dtype(at::kFloat));
+    if (q.size(0) == 0) {
+        outputs.push_back(o);
+        outputs.push_back(lse);
+        return;
+    }
+    View4 qv = MakeView4(q, "query"), kv = MakeView4(kc, "k_cache"), vv = MakeView4(vc, "v_cache");
+    at::Tensor lc = len.contiguous();
+    dtattn_decode_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = qv.t.data_ptr(), a.k_cache = kv.t.data_ptr(), a.v_cache = vv.t.data_ptr();
+    a.lengths = lc.data_ptr<int32_t>();
+    a.o = o.data_ptr(), a.lse = lse.data_ptr<float>();
+    a.B = qv.B, a.Hq = qv.H, a.Hkv = kv.H, a.S_max = kv.S, a.D = qv.D;
+    a.q_stride[0] = qv.sb, a.q_stride[1] = qv.sh;
+    a.k_stride[0] = kv.sb, a.k_stride[1] = kv.sh, a.k_stride[2] = kv.ss;
+    a.v_stride[0] = vv.sb, a.v_stride[1] = vv.sh, a.v_stride[2] = vv.ss;
+    a.o_stride[0] = q.size(1) * q.size(3), a.o_stride[1] = q.size(3);
+    a.lse_stride[0] = q.size(1);
+    a.dtype = DtypeCode(st);
+    a.scale = mScale.has_value() ? (float)mScale.value() : 0.f;
+    a.chunk = mChunk;
+    const size_t ws = dtattn_decode_workspace_size(a.B, a.Hq, a.S_max, a.D, a.chunk);
+    at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, q.options().dtype(at::kByte));
+    a.workspace = wst.data_ptr();
+    a.workspace_bytes = ws;
+    Check(dtattn_decode_splitkv(&a, CurrentStream(q)), "dtattn_decode_splitkv");
+    outputs.push_back(o);
+    outputs.push_back(lse);
+}
+
+void LseMergeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
+    if (inputs.empty() || inputs.size() % 2 != 0) Throw("LseMergeOp expects pairs {O_0, LSE_0, O_1, LSE_1, ...}");
+    const int n = (int)inputs.size() / 2;
+    if (n > DTATTN_MAX_MERGE_BLOCKS) Throw("too many blocks to merge");
+    std::vector<const at::Tensor*> all;
+    for (const auto& t : inputs) {
+        if (!t.has_value() || !t->defined()) Throw("merge inputs must all be present");
+        all.push_back(&*t);
+    }
+    CheckDevice(all);
+    const at::Tensor& o0 = *inputs[0];
+    c10::DeviceGuard guard(o0.device());
+    const c10::ScalarType st = o0.scalar_type();
+    if (DtypeCode(st) < 0 || st == at::kFloat8_e4m3fn) Throw("merge blocks must be bf16, fp16 or fp32");
+    std::vector<View4> os;
+    std::vector<at::Tensor> lses;
+    for (int i = 0; i < n; ++i) {
+        const at::Tensor& oi = *inputs[2 * i];
+        const at::Tensor& li = *inputs[2 * i + 1];
+        if (oi.sizes() != o0.sizes() || oi.scalar_type() != st) Throw("merge blocks must share shape and dtype");
+        std::vector<int64_t> ls(o0.sizes().begin(), o0.sizes().end() - 1);
+        if (li.sizes().vec() != ls || li.scalar_type() != at::kFloat) Throw("LSE blocks must be fp32 [..., H, S]");
+        os.push_back(MakeView4(oi, "O block"));
+        lses.push_back(li.contiguous());
+    }
+    // all blocks must share strides after normalisation
+    for (int i = 1; i < n; ++i)
+        if (os[i].sb != os[0].sb || os[i].sh != os[0].sh || os[i].ss != os[0].ss) {
+            for (auto& v : os) v = MakeView4(v.t.contiguous(), "O block");
+            break;
+        }
+    const c10::ScalarType ost = mOutDtype.value_or(st);
+    if (ost != at::kBFloat16 && ost != at::kHalf && ost != at::kFloat) Throw("merge output must be bf16, fp16 or fp32");
+    at::Tensor o = at::empty(o0.sizes(), o0.options().dtype(ost));
+    std::vector<int64_t> ls(o0.sizes().begin(), o0.sizes().end() - 1);
+    at::Tensor lse = at::empty(ls, o0.options().dtype(at::kFloat));
+    if (o.numel() == 0) {
+        outputs.push_back(o);
+        outputs.push_back(lse);
+        return;
+    }
+    View4 ov = MakeView4(o, "output");
+    dtattn_merge_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.n_blocks = n;
+    for (int i = 0; i < n; ++i) {
+        a.o_blocks[i] = os[i].t.data_ptr();
+        a.lse_blocks[i] = lses[i].data_ptr<float>();
+    }
+    a.B = ov.B, a.H = ov.H, a.S = ov.S, a.D = ov.D;
+    a.block_o_stride[0] = os[0].sb, a.block_o_stride[1] = os[0].sh, a.block_o_stride[2] = os[0].ss;
+    a.block_lse_stride[0] = ov.H * ov.S, a.block_lse_stride[1] = ov.S;
+    a.block_dtype = DtypeCode(st);
+    a.o = ov.t.data_ptr();
+    a.lse = lse.data_ptr<float>();
+    a.o_stride[0] = ov.sb, a.o_stride[1] = ov.sh, a.o_stride[2] = ov.ss;
+    a.lse_stride[0] = ov.H * ov.S, a.lse_stride[1] = ov.S;
+    a.o_dtype = DtypeCode(ost);
+    Check(dtattn_lse_merge(&a, CurrentStream(o0)), "dtattn_lse_merge");
+    outputs.push_back(o);
+    outputs.push_back(lse);
+}
+
+void Fp8QuantizeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
+    if (inputs.size() != 1 || !inputs[0] || !inputs[0]->defined()) Throw("Fp8QuantizeOp expects {x}");
+    const at::Tensor& x_ = *inputs[0];
+    CheckDevice({&x_});
+    c10::DeviceGuard guard(x_.device());
+    const int32_t code = DtypeCode(x_.scalar_type());
+    if (code != DTATTN_BF16 && code != DTATTN_FP16 && code != DTATTN_FP32) Throw("quantize takes bf16, fp16 or fp32");
+    View4 x = MakeView4(x_, "x");
+    at::Tensor codes = at::empty(x_.sizes(), x_.options().dtype(at::kFloat8_e4m3fn));
+    std::vector<int64_t> ds(x_.sizes().begin(), x_.sizes().end() - 2);
+    at::Tensor desc = at::empty(ds, x_.options().dtype(at::kFloat));
+    if (codes.numel() > 0) {
+        const size_t ws = dtattn_fp8_quantize_workspace_size(x.B, x.H, x.S, x.D);
+        at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, x_.options().dtype(at::kByte));
+        const int64_t strides[3] = {x.sb, x.sh, x.ss};
+        Check(dtattn_fp8_quantize_per_head(x.t.data_ptr(), code, x.B, x.H, x.S, x.D, strides, codes.data_ptr(),
+                                           desc.data_ptr<float>(), wst.data_ptr(), ws, CurrentStream(x_)),
+              "dtattn_fp8_quantize_per_head");
+    }
+    outputs.push_back(codes);
+    outputs.push_back(desc);
+}
+
+DevicePeaks GetDevicePeaks(int device) {
+    dtattn_device_peaks pk;
+    Check(dtattn_get_device_peaks(device, &pk), "dtattn_get_device_peaks");
+    return {pk.cu_count, pk.clock_hz, pk.bf16_flops, pk.fp8_flops, pk.hbm_bytes_per_s, std::string(pk.arch)};
+}
+
+}  // namespace core
+}  // namespace dtorch_amd

@@ -1,0 +1,138 @@
+// Host-side operators of the MI355X attention path, mirroring DTorch's operator contract.
+//
+// The reference's SdpaOp (dtorch/core/operators/standard/scaled_dot_product_attention_op.h:14-52)
+// exposes InferOutputMetaInfo / GetPlacementSignature / GetOperatorCost / Compute, with
+// Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) pushing freshly allocated
+// outputs.  The classes here keep those names, argument meanings and error behaviour
+// (std::invalid_argument on bad input, as Kernel::Run expects: dtorch/core/kernel/kernel.cc:140-148),
+// and route the arithmetic through the dtattn C ABI on the thread's current HIP stream.
+//
+// New operators (no reference counterpart; registered the same way an operator is added to DTorch):
+//   SdpaWithLseOp  -> {O, LSE}, with explicit causal offsets for ring blocks
+//   SdpaDecodeOp   -> {O, LSE} for one query token per sequence against a padded KV cache
+//   LseMergeOp     -> {O, LSE} from n (O_b, LSE_b) pairs
+//   Fp8QuantizeOp  -> {codes, descale}, per-head absmax e4m3fn
+#pragma once
+
+#include <torch/torch.h>
+
+#include <optional>
+#include <string>
+#include <vector>
+
+namespace dtorch_amd {
+namespace core {
+
+// dtorch/external/torch/torch_util.h:107-108
+using TorchTensorOptArray = std::vector<std::optional<::torch::Tensor>>;
+using TorchTensorArray = std::vector<::torch::Tensor>;
+
+// dtorch/api/cpp/functional/functional_option.h:19-30, plus the native fp8 selector.
+// sageAttentionType: "" (native bf16/fp16), "native_fp8" (per-head e4m3fn on fp8 MFMA), or one of the
+// reference's third-party SageAttention values ("auto", "qk_int8_pv_fp8", "qk_int8_pv_fp16"), which
+// this build does not ship and rejects.
+struct SdpaOption {
+    std::string sageAttentionType;
+    SdpaOption() : sageAttentionType("") {}
+    explicit SdpaOption(std::string t) : sageAttentionType(std::move(t)) {}
+};
+
+// dtorch/core/operators/standard/scaled_dot_product_attention_op.h:14-36 (same fields, same defaults).
+struct SdpaParam {
+    bool isCausal = false;
+    std::optional<double> scale = std::nullopt;
+    bool enableGqa = false;
+    std::optional<SdpaOption> option = std::nullopt;
+
+    SdpaParam() = default;
+    SdpaParam(bool isCausal_, std::optional<double> scale_, bool enableGqa_, std::optional<SdpaOption> option_)
+        : isCausal(isCausal_), scale(scale_), enableGqa(enableGqa_), option(std::move(option_)) {}
+};
+
+// One allowed input->output placement assignment for one mesh dimension.  Placements are written
+// "S(i)" (shard on tensor dim i), "R" (replicate); an empty string in `inputs` marks an optional input.
+struct PlacementRule {
+    std::vector<std::string> inputs;
+    std::vector<std::string> outputs;
+    std::vector<bool> optional;
+};
+using PlacementSignature = std::vector<PlacementRule>;
+
+using Shape = std::vector<int64_t>;
+
+class SdpaOp {
+public:
+    explicit SdpaOp(SdpaParam param) : mParam(std::move(param)) {}
+    virtual ~SdpaOp() = default;
+
+    const SdpaParam& Param() const { return mParam; }
+
+    // scaled_dot_product_attention_op.cc:16-32: q's shape with the last axis replaced by v's.
+    Shape InferOutputMetaInfo(const Shape& q, const Shape& k, const Shape& v) const;
+    // scaled_dot_product_attention_op.cc:34-66 plus the all-Replicate rule of
+    // placement_signature.cc:65-88.
+    PlacementSignature GetPlacementSignature(size_t numAxis) const;
+    // Output placements for one mesh dimension, or an exception when no rule matches.  `inputs`
+    // holds q, k, v, mask placements ("" for an absent mask).
+    std::vector<std::string> MatchPlacements(size_t numAxis, const std::vector<std::string>& inputs) const;
+    // scaled_dot_product_attention_op.cc:68-95: 2 * batch * qHeads * seqQ * seqKv * (headDim + Ev).
+    int64_t GetOperatorCost(const Shape& q, const Shape& k, const Shape& v) const;
+    // Useful FLOPs (causal counts only visible pairs, diagonal included); used for roofline figures.
+    int64_t GetAlgorithmicFlops(const Shape& q, const Shape& k, const Shape& v) const;
+
+    // inputs = {q, k, v, attn_mask?}; pushes O.
+    virtual void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
+
+protected:
+    SdpaParam mParam;
+};
+
+// {q, k, v, attn_mask?} -> {O, LSE[B, Hq, Sq] fp32}; key j visible to query i iff
+// j + kOffset <= i + qOffset when causal.
+class SdpaWithLseOp : public SdpaOp {
+public:
+    SdpaWithLseOp(SdpaParam param, int64_t qOffset, int64_t kOffset)
+        : SdpaOp(std::move(param)), mQOffset(qOffset), mKOffset(kOffset) {}
+    void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const override;
+
+private:
+    int64_t mQOffset, mKOffset;
+};
+
+// {q[B,Hq,1,D], k_cache[B,Hkv,S,D], v_cache[B,Hkv,S,D], lengths[B] int32} -> {O[B,Hq,1,D], LSE[B,Hq]}
+class SdpaDecodeOp {
+public:
+    SdpaDecodeOp(std::optional<double> scale, int32_t chunk) : mScale(scale), mChunk(chunk) {}
+    void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
+
+private:
+    std::optional<double> mScale;
+    int32_t mChunk;
+};
+
+// {O_0, LSE_0, O_1, LSE_1, ...} -> {O, LSE}; O in `outDtype` (default: the blocks' dtype).
+class LseMergeOp {
+public:
+    explicit LseMergeOp(std::optional<c10::ScalarType> outDtype = std::nullopt) : mOutDtype(outDtype) {}
+    void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
+
+private:
+    std::optional<c10::ScalarType> mOutDtype;
+};
+
+// {x[B,H,S,D]} -> {codes[B,H,S,D] float8_e4m3fn, descale[B,H] fp32}
+class Fp8QuantizeOp {
+public:
+    void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
+};
+
+// MI355X peak table of the current device (native analog of DevicePeakPerformance).
+struct DevicePeaks {
+    int cuCount;
+    double clockHz, bf16Flops, fp8Flops, hbmBytesPerS;
+    std::string arch;
+};
+DevicePeaks GetDevicePeaks(int device);
+
+}  // namespace core
+}  // namespace dtorch_amd

@@ -1,0 +1,185 @@
+// LSE merge of n partial attention blocks (the combine step of blockwise ring attention).
+//
+// No counterpart in the reference: its ring context parallelism all-gathers K/V and runs one SDPA
+// (python/dtorch/nn/scaled_dot_product_attention_with_cp.py:87-101).  Closed form, per query row:
+//   m = max_b LSE_b,  LSE = m + log sum_b exp(LSE_b - m),  O = sum_b exp(LSE_b - LSE) O_b.
+// HBM-bound: one thread per 16-byte output chunk (8 elements); each thread reads the n LSE values of
+// its row (shared by the D/8 threads of the row through L1) and n input chunks, and writes one chunk.
+#include "dtattn_common.hpp"
+
+namespace dtattn {
+
+struct MergeParams {
+    const void* o_blocks[DTATTN_MAX_MERGE_BLOCKS];
+    const float* lse_blocks[DTATTN_MAX_MERGE_BLOCKS];
+    void* o;
+    float* lse;
+    int64_t bo_b, bo_h, bo_s;
+    int64_t bl_b, bl_h;
+    int64_t o_b, o_h, o_s;
+    int64_t l_b, l_h;
+    int64_t rows;  // B * H * S
+    int32_t H, S, n;
+};
+
+template <typename TI>
+__device__ __forceinline__ void load8(const TI* p, float* out);
+template <>
+__device__ __forceinline__ void load8<bf16_t>(const bf16_t* p, float* out) {
+    unpack8<bf16_t>(ld16(p), out);
+}
+template <>
+__device__ __forceinline__ void load8<f16_t>(const f16_t* p, float* out) {
+    unpack8<f16_t>(ld16(p), out);
+}
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float* out) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+    out[0] = a.x, out[1] = a.y, out[2] = a.z, out[3] = a.w;
+    out[4] = b.x, out[5] = b.y, out[6] = b.z, out[7] = b.w;
+}
+
+template <typename TO>
+__device__ __forceinline__ void store8(TO* p, const float* in);
+template <>
+__device__ __forceinline__ void store8<bf16_t>(bf16_t* p, const float* in) {
+    st16(p, pack8<bf16_t>(in));
+}
+template <>
+__device__ __forceinline__ void store8<f16_t>(f16_t* p, const float* in) {
+    st16(p, pack8<f16_t>(in));
+}
+template <>
+__device__ __forceinline__ void store8<float>(float* p, const float* in) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{in[0], in[1], in[2], in[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{in[4], in[5], in[6], in[7]};
+}
+
+template <typename TI, typename TO, int D, int NB>
+__global__ void __launch_bounds__(256) lse_merge_kernel(const MergeParams p) {
+    constexpr int CPR = D / 8;  // chunks per row
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t row = gid / CPR;
+    if (row >= p.rows) return;
+    const int c = (int)(gid % CPR);
+    const int s = (int)(row % p.S);
+    const int64_t bh = row / p.S;
+    const int h = (int)(bh % p.H);
+    const int64_t b = bh / p.H;
+    const int n = NB > 0 ? NB : p.n;
+
+    float l[DTATTN_MAX_MERGE_BLOCKS];
+    float m = kNegInf;
+#pragma unroll
+    for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) {
+        if (i >= n) break;
+        l[i] = p.lse_blocks[i][b * p.bl_b + h * p.bl_h + s];
+        m = fmaxf(m, l[i]);
+    }
+    const float mb = m == kNegInf ? 0.f : m;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) {
+        if (i >= n) break;
+        l[i] = __expf(l[i] - mb);
+        sum += l[i];
+    }
+    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int64_t in_off = b * p.bo_b + h * p.bo_h + (int64_t)s * p.bo_s + c * 8;
+#pragma unroll
+    for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) {
+        if (i >= n) break;
+        const float w = l[i] * inv;
+        if (w == 0.f) continue;  // a block with LSE = -inf is a no-op (its O may be anything)
+        float x[8];
+        load8<TI>(reinterpret_cast<const TI*>(p.o_blocks[i]) + in_off, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(w, x[e], acc[e]);
+    }
+    store8<TO>(reinterpret_cast<TO*>(p.o) + b * p.o_b + h * p.o_h + (int64_t)s * p.o_s + c * 8, acc);
+    if (p.lse != nullptr && c == 0) p.lse[b * p.l_b + h * p.l_h + s] = sum > 0.f ? mb + __logf(sum) : kNegInf;
+}
+
+template <typename TI, typename TO, int D>
+static int launch_merge(const MergeParams& p, hipStream_t stream) {
+    const int64_t threads = p.rows * (D / 8);
+    const int64_t blocks = (threads + 255) / 256;
+    if (blocks == 0) return DTATTN_OK;
+    if (blocks > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "merge: grid too large");
+    switch (p.n) {
+        case 2:
+            hipLaunchKernelGGL((lse_merge_kernel<TI, TO, D, 2>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+            break;
+        case 4:
+            hipLaunchKernelGGL((lse_merge_kernel<TI, TO, D, 4>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+            break;
+        default:
+            hipLaunchKernelGGL((lse_merge_kernel<TI, TO, D, 0>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+            break;
+    }
+    return check_launch("lse_merge_kernel");
+}
+
+template <typename TI, typename TO>
+static int dispatch_merge_d(const MergeParams& p, int D, hipStream_t stream) {
+    if (D == 128) return launch_merge<TI, TO, 128>(p, stream);
+    if (D == 64) return launch_merge<TI, TO, 64>(p, stream);
+    return fail(DTATTN_ERR_UNSUPPORTED, "merge: head dim %d not supported (64 or 128)", D);
+}
+
+template <typename TI>
+static int dispatch_merge_o(const MergeParams& p, int D, int o_dtype, hipStream_t stream) {
+    if (o_dtype == DTATTN_BF16) return dispatch_merge_d<TI, bf16_t>(p, D, stream);
+    if (o_dtype == DTATTN_FP16) return dispatch_merge_d<TI, f16_t>(p, D, stream);
+    if (o_dtype == DTATTN_FP32) return dispatch_merge_d<TI, float>(p, D, stream);
+    return fail(DTATTN_ERR_UNSUPPORTED, "merge: output dtype %d not supported", o_dtype);
+}
+
+}  // namespace dtattn
+
+using namespace dtattn;
+
+extern "C" int dtattn_lse_merge(const dtattn_merge_args* a, void* stream_) {
+    if (a == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: args is NULL");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (a->n_blocks < 1 || a->n_blocks > DTATTN_MAX_MERGE_BLOCKS)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: n_blocks=%d outside [1, %d]", a->n_blocks,
+                    DTATTN_MAX_MERGE_BLOCKS);
+    if (a->B < 0 || a->H < 0 || a->S < 0 || a->D <= 0) return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: bad sizes");
+    if (a->B == 0 || a->H == 0 || a->S == 0) return DTATTN_OK;
+    if (a->S > 0x7fffffff || a->H > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "merge: sizes too large");
+    if (a->o == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: null output");
+    const int in_esz = a->block_dtype == DTATTN_FP32 ? 4 : 2;
+    const int out_esz = a->o_dtype == DTATTN_FP32 ? 4 : 2;
+    for (int j = 0; j < 3; ++j) {
+        if ((a->block_o_stride[j] * in_esz) % 16 != 0 || (a->o_stride[j] * out_esz) % 16 != 0)
+            return fail(DTATTN_ERR_UNSUPPORTED, "merge: strides must be multiples of 16 bytes");
+    }
+    MergeParams p;
+    for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) {
+        p.o_blocks[i] = i < a->n_blocks ? a->o_blocks[i] : nullptr;
+        p.lse_blocks[i] = i < a->n_blocks ? a->lse_blocks[i] : nullptr;
+        if (i < a->n_blocks && (p.o_blocks[i] == nullptr || p.lse_blocks[i] == nullptr))
+            return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: block %d has a null pointer", i);
+        if (i < a->n_blocks && (reinterpret_cast<uintptr_t>(p.o_blocks[i]) & 15u) != 0)
+            return fail(DTATTN_ERR_UNSUPPORTED, "merge: block %d is not 16-byte aligned", i);
+    }
+    p.o = a->o;
+    p.lse = a->lse;
+    p.bo_b = a->block_o_stride[0], p.bo_h = a->block_o_stride[1], p.bo_s = a->block_o_stride[2];
+    p.bl_b = a->block_lse_stride[0], p.bl_h = a->block_lse_stride[1];
+    p.o_b = a->o_stride[0], p.o_h = a->o_stride[1], p.o_s = a->o_stride[2];
+    p.l_b = a->lse ? a->lse_stride[0] : 0;
+    p.l_h = a->lse ? a->lse_stride[1] : 0;
+    p.rows = a->B * a->H * a->S;
+    p.H = (int32_t)a->H;
+    p.S = (int32_t)a->S;
+    p.n = a->n_blocks;
+    const int D = (int)a->D;
+    if (a->block_dtype == DTATTN_BF16) return dispatch_merge_o<bf16_t>(p, D, a->o_dtype, stream);
+    if (a->block_dtype == DTATTN_FP16) return dispatch_merge_o<f16_t>(p, D, a->o_dtype, stream);
+    if (a->block_dtype == DTATTN_FP32) return dispatch_merge_o<float>(p, D, a->o_dtype, stream);
+    return fail(DTATTN_ERR_UNSUPPORTED, "merge: block dtype %d not supported", a->block_dtype);
+}

@@ -1,0 +1,447 @@
+// Flash-style attention forward for gfx950 (bf16 / fp16 MFMA), with per-row LSE.
+//
+// Replaces the arithmetic of SdpaOp::Compute (the libtorch call at
+// dtorch/core/operators/standard/scaled_dot_product_attention_op.cc:107-109) on the GPU.
+//
+// Work decomposition
+//   One workgroup = 4 waves = 4*QT*32 consecutive query rows of one (batch, query head).  Each wave
+//   owns QT tiles of 32 queries and keeps their Q fragments in registers for the whole kernel.
+//   Key/value tiles of 64 rows are staged through LDS and shared by the 4 waves.
+//
+// Layout trick
+//   The score tile is computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_{bf16,f16}: the
+//   accumulator column (lane % 32) is the query, so each lane holds 16 keys of one query row and the
+//   row max / row sum need one cross-half exchange (lane ^ 32) instead of a 32-lane reduction.  The
+//   output is accumulated transposed as well, O^T = V^T P^T: P^T comes straight from the score
+//   registers (the MFMA reduction index is a free permutation, matched on both operands), and V is
+//   written transposed into LDS so each lane reads 4 consecutive keys of one d with one 8-byte read.
+//   The per-query rescale factor is then a per-lane scalar.
+//
+// LDS layouts (bank-conflict free for the 16-byte K reads and the 8-byte V^T reads/writes)
+//   K  tile: [64 keys][D], 16-byte chunk c of row r stored at chunk c ^ kswz(r).
+//   V^T tile: [D][64 keys], 4-key group g of row d stored at group g ^ ((d & 15) ^ ((d >> 4) & 15)).
+//
+// Pipeline per key tile j (one LDS buffer each for K and V^T, register prefetch one tile ahead):
+//   barrier | prefetch K[j+1] -> regs | S = K[j] Q^T | V[j] regs -> LDS | softmax |
+//   barrier | K[j+1] regs -> LDS | prefetch V[j+1] -> regs | O^T += V^T P^T
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "dtattn_common.hpp"
+
+namespace dtattn {
+
+struct PrefillParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    int64_t qs_b, qs_h, qs_s;
+    int64_t ks_b, ks_h, ks_s;
+    int64_t vs_b, vs_h, vs_s;
+    int64_t os_b, os_h, os_s;
+    int64_t lses_b, lses_h;
+    int32_t B, Hq, Hkv, Sq, Sk, group;
+    int32_t n_qblocks;
+    int32_t delta;  // key j visible to query i iff j <= i + delta (causal only)
+    float c;        // softmax scale * log2(e)
+};
+
+template <int D>
+__device__ __forceinline__ int kswz(int r) {
+    return D >= 128 ? (r & 15) : (r & 7);
+}
+
+__device__ __forceinline__ int vswz(int d) { return (d & 15) ^ ((d >> 4) & 15); }
+
+// Pack the (e)-th 16-bit half of two dwords into one dword: low half from a, high half from b.
+__device__ __forceinline__ uint32_t pack_half(uint32_t a, uint32_t b, int e) {
+    return __builtin_amdgcn_perm(b, a, e ? 0x07060302u : 0x05040100u);
+}
+
+template <typename T, int D, int QT, bool CAUSAL>
+__global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams p) {
+    constexpr int NW = 4;
+    constexpr int BN = 64;
+    constexpr int BM = NW * QT * 32;
+    constexpr int DCH = D / 8;            // 16-byte chunks per row
+    constexpr int KSTEPS = D / 16;        // MFMA k-steps of S = K Q^T
+    constexpr int DT = D / 32;            // 32-row d tiles of O^T
+    constexpr int KT = BN / 32;           // 32-key tiles per key block
+    constexpr int PVS = BN / 16;          // MFMA k-steps of O^T = V^T P^T
+    constexpr int KPT = BN * DCH / 256;   // K chunks per thread
+    constexpr int NVB = (BN / 4) * DCH;   // 4-key x 8-d blocks of V per tile
+    constexpr int OSTR = D + 8;           // staging row stride (elements)
+    constexpr int KV_BYTES = 2 * BN * D * 2;
+    constexpr int O_BYTES = NW * QT * 32 * OSTR * 2;
+    constexpr int SMEM = KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES;
+    static_assert(KPT >= 1 && (BN * DCH) % 256 == 0, "tile/thread mismatch");
+    static_assert(NVB <= 256, "one V block per thread at most");
+    typedef typename Elem<T>::vec8 V8;
+
+    __shared__ __attribute__((aligned(16))) char smem[SMEM];
+    T* Ks = reinterpret_cast<T*>(smem);
+    T* VTs = Ks + BN * D;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int hf = lane >> 5;
+
+    const int bh = p.B * p.Hq;
+    const int bid = blockIdx.x;
+    const int qb = CAUSAL ? (p.n_qblocks - 1 - bid / bh) : (bid / bh);
+    const int rest = bid % bh;
+    const int hq = rest % p.Hq;
+    const int b = rest / p.Hq;
+    const int hk = hq / p.group;
+
+    const T* qp = reinterpret_cast<const T*>(p.q) + b * p.qs_b + hq * p.qs_h;
+    const T* kp = reinterpret_cast<const T*>(p.k) + b * p.ks_b + hk * p.ks_h;
+    const T* vp = reinterpret_cast<const T*>(p.v) + b * p.vs_b + hk * p.vs_h;
+
+    const int q0 = qb * BM;
+    const int wq0 = q0 + wave * QT * 32;
+
+    int kend = p.Sk;
+    if (CAUSAL) {
+        const int64_t lim = (int64_t)q0 + BM + p.delta;  // keys < lim can be visible
+        kend = (int)(lim < 0 ? 0 : (lim < p.Sk ? lim : p.Sk));
+    }
+    const int nt = (kend + BN - 1) / BN;
+
+    // Q fragments (B operand of S^T = K Q^T): lane holds query l32, d = ks*16 + hf*8 .. +8.
+    V8 qf[QT][KSTEPS];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int qrow = wq0 + qt * 32 + l32;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            u32x4 raw = {0u, 0u, 0u, 0u};
+            if (qrow < p.Sq) raw = ld16(qp + (int64_t)qrow * p.qs_s + ks * 16 + hf * 8);
+            qf[qt][ks] = __builtin_bit_cast(V8, raw);
+        }
+    }
+
+    f32x16 oacc[QT][DT];
+    float mrow[QT], lrow[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        mrow[qt] = kNegInf;
+        lrow[qt] = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[qt][dt][i] = 0.f;
+    }
+
+    u32x4 kreg[KPT];
+    u32x4 vreg[4];
+
+    auto load_k = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int id = i * 256 + tid;
+            const int r = id / DCH, c = id % DCH;
+            const int key = t * BN + r;
+            u32x4 raw = {0u, 0u, 0u, 0u};
+            if (key < p.Sk) raw = ld16(kp + (int64_t)key * p.ks_s + c * 8);
+            kreg[i] = raw;
+        }
+    };
+    auto store_k = [&]() {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int id = i * 256 + tid;
+            const int r = id / DCH, c = id % DCH;
+            st16(Ks + r * D + 8 * (c ^ kswz<D>(r)), kreg[i]);
+        }
+    };
+    auto load_v = [&](int t) {
+        if (tid < NVB) {
+            const int g = tid / DCH, c = tid % DCH;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = t * BN + 4 * g + i;
+                u32x4 raw = {0u, 0u, 0u, 0u};
+                if (key < p.Sk) raw = ld16(vp + (int64_t)key * p.vs_s + c * 8);
+                vreg[i] = raw;
+            }
+        }
+    };
+    auto store_v = [&]() {
+        if (tid < NVB) {
+            const int g = tid / DCH, c = tid % DCH;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int d = c * 8 + 2 * w + e;
+                    u32x2 pr;
+                    pr.x = pack_half(vreg[0][w], vreg[1][w], e);
+                    pr.y = pack_half(vreg[2][w], vreg[3][w], e);
+                    *reinterpret_cast<u32x2*>(VTs + d * BN + 4 * (g ^ vswz(d))) = pr;
+                }
+            }
+        }
+    };
+
+    if (nt > 0) {
+        load_k(0);
+        store_k();
+        load_v(0);
+    }
+
+    for (int t = 0; t < nt; ++t) {
+        __syncthreads();
+        if (t + 1 < nt) load_k(t + 1);
+
+        const int kbase = t * BN;
+        const bool wave_skip = CAUSAL && ((int64_t)kbase > (int64_t)wq0 + QT * 32 - 1 + p.delta);
+        const bool need_mask =
+            (kbase + BN > p.Sk) || (CAUSAL && ((int64_t)kbase + BN - 1 > (int64_t)wq0 + p.delta));
+
+        f32x16 s[QT][KT];
+        V8 pb[QT][PVS];
+        if (!wave_skip) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) s[qt][kt][i] = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt) {
+                    const int r = kt * 32 + l32;
+                    const int c = ks * 2 + hf;
+                    V8 a = *reinterpret_cast<const V8*>(Ks + r * D + 8 * (c ^ kswz<D>(r)));
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt) s[qt][kt] = Elem<T>::mfma32(a, qf[qt][ks], s[qt][kt]);
+                }
+            }
+        }
+
+        store_v();
+
+        if (!wave_skip) {
+            if (need_mask) {
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) {
+                    const int64_t qlim = (int64_t)wq0 + qt * 32 + l32 + p.delta;
+#pragma unroll
+                    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            const int key = kbase + kt * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
+                            bool vis = key < p.Sk;
+                            if (CAUSAL) vis = vis && ((int64_t)key <= qlim);
+                            if (!vis) s[qt][kt][i] = kNegInf;
+                        }
+                }
+            }
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                float mx = kNegInf;
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[qt][kt][i]);
+                mx = fmaxf(mx, shfl_xor_f(mx, 32));
+                const float mnew = fmaxf(mrow[qt], mx * p.c);
+                const float mbase = (mnew == kNegInf) ? 0.f : mnew;
+                const float alpha = fast_exp2(mrow[qt] - mbase);
+                mrow[qt] = mnew;
+                float ls = lrow[qt] * alpha;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) oacc[qt][dt][i] *= alpha;
+#pragma unroll
+                for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+                    for (int half = 0; half < 2; ++half) {
+                        V8 pk;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const float pv = fast_exp2(__builtin_fmaf(s[qt][kt][8 * half + e], p.c, -mbase));
+                            ls += pv;
+                            pk[e] = Elem<T>::from_f32(pv);
+                        }
+                        pb[qt][2 * kt + half] = pk;
+                    }
+                }
+                lrow[qt] = ls;
+            }
+        }
+
+        __syncthreads();
+        if (t + 1 < nt) {
+            store_k();
+            load_v(t + 1);
+        }
+
+        if (!wave_skip) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int d = dt * 32 + l32;
+                const int sw = vswz(d);
+#pragma unroll
+                for (int ks = 0; ks < PVS; ++ks) {
+                    const int g1 = ks * 4 + hf, g2 = ks * 4 + 2 + hf;
+                    const u32x2 lo = *reinterpret_cast<const u32x2*>(VTs + d * BN + 4 * (g1 ^ sw));
+                    const u32x2 hi = *reinterpret_cast<const u32x2*>(VTs + d * BN + 4 * (g2 ^ sw));
+                    const u32x4 raw = {lo.x, lo.y, hi.x, hi.y};
+                    const V8 a = __builtin_bit_cast(V8, raw);
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt) oacc[qt][dt] = Elem<T>::mfma32(a, pb[qt][ks], oacc[qt][dt]);
+                }
+            }
+        }
+    }
+
+    // Epilogue: normalise, stage O through LDS for 16-byte coalesced row stores, write LSE.
+    __syncthreads();
+    T* Os = reinterpret_cast<T*>(smem) + wave * QT * 32 * OSTR;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const float l = lrow[qt] + shfl_xor_f(lrow[qt], 32);
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        const int row = qt * 32 + l32;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                typename Elem<T>::vec4 o4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o4[e] = Elem<T>::from_f32(oacc[qt][dt][4 * i4 + e] * inv);
+                *reinterpret_cast<typename Elem<T>::vec4*>(Os + row * OSTR + dt * 32 + 8 * i4 + 4 * hf) = o4;
+            }
+        if (p.lse != nullptr && hf == 0) {
+            const int qrow = wq0 + row;
+            if (qrow < p.Sq) {
+                const float lse = l > 0.f ? (mrow[qt] + __log2f(l)) * kLn2 : kNegInf;
+                p.lse[b * p.lses_b + hq * p.lses_h + qrow] = lse;
+            }
+        }
+    }
+    __syncthreads();
+    T* op = reinterpret_cast<T*>(p.o) + b * p.os_b + hq * p.os_h;
+#pragma unroll
+    for (int it = 0; it < QT * 32 * DCH / 64; ++it) {
+        const int id = it * 64 + lane;
+        const int row = id / DCH, c = id % DCH;
+        const int qrow = wq0 + row;
+        if (qrow < p.Sq) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Os + row * OSTR + c * 8));
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+
+template <typename T, int D, int QT, bool CAUSAL>
+static int launch_prefill(const PrefillParams& prm, hipStream_t stream) {
+    constexpr int BM = 4 * QT * 32;
+    PrefillParams p = prm;
+    p.n_qblocks = (p.Sq + BM - 1) / BM;
+    const int64_t grid = (int64_t)p.n_qblocks * p.B * p.Hq;
+    if (grid == 0) return DTATTN_OK;
+    if (grid > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill grid too large (%lld blocks)", (long long)grid);
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, QT, CAUSAL>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    return check_launch("prefill_fwd_kernel");
+}
+
+template <typename T>
+static int dispatch_prefill(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
+    if (D == 128) {
+        return causal ? launch_prefill<T, 128, 1, true>(p, stream) : launch_prefill<T, 128, 1, false>(p, stream);
+    }
+    if (D == 64) {
+        return causal ? launch_prefill<T, 64, 1, true>(p, stream) : launch_prefill<T, 64, 1, false>(p, stream);
+    }
+    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %d not supported (64 or 128)", D);
+}
+
+int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_t stream);
+
+static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+}  // namespace dtattn
+
+using namespace dtattn;
+
+extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
+    if (a == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill: args is NULL");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (a->B < 0 || a->Hq <= 0 || a->Hkv <= 0 || a->Sq < 0 || a->Sk < 0)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill: bad sizes B=%lld Hq=%lld Hkv=%lld Sq=%lld Sk=%lld",
+                    (long long)a->B, (long long)a->Hq, (long long)a->Hkv, (long long)a->Sq, (long long)a->Sk);
+    if (a->Hq % a->Hkv != 0)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill: Hq=%lld is not a multiple of Hkv=%lld", (long long)a->Hq,
+                    (long long)a->Hkv);
+    if (a->D != a->Dv)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: D=%lld != Dv=%lld not supported", (long long)a->D,
+                    (long long)a->Dv);
+    if (a->Sq > 0x3fffffff || a->Sk > 0x3fffffff || a->B * a->Hq > 0x3fffffff)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: sizes exceed 2^30");
+    if (a->B == 0 || a->Sq == 0) return DTATTN_OK;
+    if (a->q == nullptr || a->o == nullptr || (a->Sk > 0 && (a->k == nullptr || a->v == nullptr)))
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill: null tensor pointer");
+    const int64_t* strides[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
+    const int esz_in = a->dtype == DTATTN_FP8_E4M3FN ? 1 : 2;
+    for (int i = 0; i < 4; ++i) {
+        const int esz = i == 3 ? 2 : esz_in;
+        for (int j = 0; j < 3; ++j)
+            if ((strides[i][j] * esz) % 16 != 0)
+                return fail(DTATTN_ERR_UNSUPPORTED,
+                            "prefill: tensor %d stride[%d]=%lld is not a multiple of 16 bytes", i, j,
+                            (long long)strides[i][j]);
+    }
+    if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: tensors must be 16-byte aligned");
+    const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
+    const float c = scale * kLog2e;
+    int64_t delta64 = a->q_offset - a->k_offset;
+    const int64_t lim = a->Sq + a->Sk + 1;
+    if (delta64 > lim) delta64 = lim;
+    if (delta64 < -lim) delta64 = -lim;
+    const int32_t delta = (int32_t)delta64;
+
+    if (a->dtype == DTATTN_FP8_E4M3FN) {
+        if (a->o_dtype != DTATTN_BF16) return fail(DTATTN_ERR_UNSUPPORTED, "prefill fp8: output must be bf16");
+        if (a->q_descale == nullptr || a->k_descale == nullptr || a->v_descale == nullptr)
+            return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill fp8: descale pointers are required");
+        return prefill_fp8(a, c, delta, stream);
+    }
+    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: dtype %d not supported (bf16, fp16, fp8_e4m3fn)", a->dtype);
+    if (a->o_dtype != a->dtype) return fail(DTATTN_ERR_UNSUPPORTED, "prefill: output dtype must equal input dtype");
+
+    PrefillParams p;
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.o = a->o;
+    p.lse = a->lse;
+    p.qs_b = a->q_stride[0], p.qs_h = a->q_stride[1], p.qs_s = a->q_stride[2];
+    p.ks_b = a->k_stride[0], p.ks_h = a->k_stride[1], p.ks_s = a->k_stride[2];
+    p.vs_b = a->v_stride[0], p.vs_h = a->v_stride[1], p.vs_s = a->v_stride[2];
+    p.os_b = a->o_stride[0], p.os_h = a->o_stride[1], p.os_s = a->o_stride[2];
+    p.lses_b = a->lse ? a->lse_stride[0] : 0;
+    p.lses_h = a->lse ? a->lse_stride[1] : 0;
+    p.B = (int32_t)a->B;
+    p.Hq = (int32_t)a->Hq;
+    p.Hkv = (int32_t)a->Hkv;
+    p.Sq = (int32_t)a->Sq;
+    p.Sk = (int32_t)a->Sk;
+    p.group = (int32_t)(a->Hq / a->Hkv);
+    p.n_qblocks = 0;
+    p.delta = delta;
+    p.c = c;
+    const int D = (int)a->D;
+    const bool causal = a->causal != 0;
+    if (a->dtype == DTATTN_BF16) return dispatch_prefill<bf16_t>(p, D, causal, stream);
+    return dispatch_prefill<f16_t>(p, D, causal, stream);
+}

@@ -1,0 +1,171 @@
+/*
+ * dtattn — C ABI of the MI355X (gfx950) attention kernels behind DTorch's SdpaOp.
+ *
+ * Every entry point takes device pointers, element strides and a HIP stream passed as `void*`
+ * (a hipStream_t; NULL is the null stream).  Nothing here allocates device memory, creates or
+ * switches streams, or synchronises: work is enqueued on `stream` and the call returns.  The
+ * functions are reentrant; the only global state is a per-device property cache filled once under
+ * std::call_once.  On failure they return a non-zero dtattn_status and dtattn_last_error() gives
+ * a thread-local message (the C++ host op turns it into std::invalid_argument, the exception
+ * SdpaOp's callers already handle: dtorch/core/kernel/kernel.cc:140-148).
+ *
+ * Layout is the reference's HND, [B, H, S, D], with arbitrary strides in elements for B, H and S
+ * and a unit stride for D (scaled_dot_product_attention_op.cc:16-32 takes [..., H, S, E]).
+ */
+#ifndef DTATTN_H_
+#define DTATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DTATTN_ABI_VERSION 1
+
+typedef enum {
+    DTATTN_OK = 0,
+    DTATTN_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad shape/stride, head counts that do not divide */
+    DTATTN_ERR_UNSUPPORTED = 2,      /* valid request the kernels do not implement (dtype, head dim) */
+    DTATTN_ERR_WORKSPACE = 3,        /* workspace missing or smaller than dtattn_*_workspace_size() */
+    DTATTN_ERR_LAUNCH = 4,           /* the HIP launch itself failed */
+    DTATTN_ERR_DEVICE = 5            /* HIP device query failed */
+} dtattn_status;
+
+typedef enum {
+    DTATTN_BF16 = 0,
+    DTATTN_FP16 = 1,
+    DTATTN_FP8_E4M3FN = 2, /* OCP e4m3fn, max 448, per-head descales */
+    DTATTN_FP32 = 3
+} dtattn_dtype;
+
+/* Prefill / per-block attention: O = softmax(scale * Q K^T [causal]) V, plus the per-row LSE.
+ *
+ * Replaces the arithmetic of SdpaOp::Compute, i.e. the libtorch call at
+ * dtorch/core/operators/standard/scaled_dot_product_attention_op.cc:107-109
+ * (torch::scaled_dot_product_attention(q, k, v, mask, 0.0, isCausal, scale, enableGqa)), for
+ * mask == nullopt.  GQA: query head h reads kv head h / (Hq / Hkv) (the op's enableGqa and the
+ * Llama port's repeat_kv, python/dtorch/test/modules/llama.py:80-85).  Causal rule: key j is
+ * visible to query i iff j + k_offset <= i + q_offset; (0, 0) is torch's top-left alignment, a ring
+ * block uses the chunks' global offsets.  Rows that see no key get O = 0 and LSE = -inf.
+ *
+ * dtype: BF16 or FP16 (inputs and output), or FP8_E4M3FN inputs with descales and a BF16 output.
+ * Head dims: D == Dv, D in {64, 128}.
+ */
+typedef struct {
+    const void* q; /* [B, Hq, Sq, D] */
+    const void* k; /* [B, Hkv, Sk, D] */
+    const void* v; /* [B, Hkv, Sk, Dv] */
+    void* o;       /* [B, Hq, Sq, Dv], dtype `o_dtype` */
+    float* lse;    /* [B, Hq, Sq] natural-log LSE, fp32; may be NULL */
+    int64_t B, Hq, Hkv, Sq, Sk, D, Dv;
+    int64_t q_stride[3]; /* element strides of B, H, S (D stride is 1) */
+    int64_t k_stride[3];
+    int64_t v_stride[3];
+    int64_t o_stride[3];
+    int64_t lse_stride[2]; /* B, H (S stride is 1) */
+    int32_t dtype;   /* dtattn_dtype of q, k, v */
+    int32_t o_dtype; /* dtattn_dtype of o: equal to dtype, or BF16 when dtype is FP8_E4M3FN */
+    float scale;     /* softmax scale; <= 0 means 1/sqrt(D) */
+    int32_t causal;
+    int64_t q_offset, k_offset;
+    const float* q_descale; /* FP8 only: [B, Hq] fp32, real = code * descale */
+    const float* k_descale; /* FP8 only: [B, Hkv] */
+    const float* v_descale; /* FP8 only: [B, Hkv] */
+} dtattn_prefill_args;
+
+int dtattn_prefill_fwd(const dtattn_prefill_args* args, void* stream);
+
+/* Split-KV single-token decode against a padded per-sequence KV cache.
+ *
+ * No counterpart in the reference (it has no KV cache, python/dtorch/test/modules/llama.py:126-156);
+ * defined as SdpaOp::Compute's arithmetic (scaled_dot_product_attention_op.cc:107-109) with Lq = 1,
+ * is_causal = False and GQA, over keys [0, lengths[b]).  Cache rows at or past lengths[b] are never
+ * read.  Each (b, kv head, chunk of `chunk` tokens) is one work item writing a partial (O, LSE)
+ * into the workspace; a second kernel merges the partials by LSE.
+ */
+typedef struct {
+    const void* q;         /* [B, Hq, 1, D] */
+    const void* k_cache;   /* [B, Hkv, S_max, D] */
+    const void* v_cache;   /* [B, Hkv, S_max, D] */
+    const int32_t* lengths;/* [B] device int32, 1 <= lengths[b] <= S_max */
+    void* o;               /* [B, Hq, 1, D], same dtype as q */
+    float* lse;            /* [B, Hq] fp32; may be NULL */
+    int64_t B, Hq, Hkv, S_max, D;
+    int64_t q_stride[2];   /* B, H */
+    int64_t k_stride[3];   /* B, H, S */
+    int64_t v_stride[3];
+    int64_t o_stride[2];   /* B, H */
+    int64_t lse_stride[1]; /* B (H stride is 1) */
+    int32_t dtype;         /* BF16 or FP16 */
+    float scale;           /* <= 0 means 1/sqrt(D) */
+    int32_t chunk;         /* tokens per split, multiple of 64; 0 picks the default (256) */
+    void* workspace;       /* >= dtattn_decode_workspace_size(...) bytes, 256-byte aligned */
+    size_t workspace_bytes;
+} dtattn_decode_args;
+
+size_t dtattn_decode_workspace_size(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk);
+int dtattn_decode_splitkv(const dtattn_decode_args* args, void* stream);
+
+/* LSE merge of n partial attention blocks over the same queries.
+ *
+ * No counterpart in the reference: its ring context parallelism all-gathers K/V and runs one SDPA
+ * (python/dtorch/nn/scaled_dot_product_attention_with_cp.py:87-101); this is the combine step of
+ * the blockwise ring.  With m = max_b LSE_b: LSE = m + log sum_b exp(LSE_b - m) and
+ * O = sum_b exp(LSE_b - LSE) O_b.  Blocks with LSE = -inf contribute nothing.
+ * All blocks share one shape [B, H, S, D] and one set of strides.
+ */
+#define DTATTN_MAX_MERGE_BLOCKS 16
+typedef struct {
+    int32_t n_blocks;                            /* 1 .. DTATTN_MAX_MERGE_BLOCKS */
+    const void* o_blocks[DTATTN_MAX_MERGE_BLOCKS];   /* each [B, H, S, D] */
+    const float* lse_blocks[DTATTN_MAX_MERGE_BLOCKS];/* each [B, H, S] fp32 */
+    int64_t B, H, S, D;
+    int64_t block_o_stride[3];  /* B, H, S */
+    int64_t block_lse_stride[2];/* B, H */
+    int32_t block_dtype;        /* BF16, FP16 or FP32 */
+    void* o;                    /* [B, H, S, D] */
+    float* lse;                 /* [B, H, S]; may be NULL */
+    int64_t o_stride[3];
+    int64_t lse_stride[2];
+    int32_t o_dtype;            /* BF16, FP16 or FP32 */
+} dtattn_merge_args;
+
+int dtattn_lse_merge(const dtattn_merge_args* args, void* stream);
+
+/* Per-head absmax quantization to fp8 e4m3fn (the pre-pass of the fp8 prefill).
+ *
+ * Supersedes the reference's SageAttention branch, which quantizes inside a third-party Python
+ * package (dtorch/external/sage_attn/sage_attn_adapter.cc:28-158).  For each (b, h):
+ * amax = max |x|; inv = 448 / amax; code = e4m3fn_rne(x * inv) (saturating); descale = amax / 448;
+ * amax == 0 gives inv = descale = 1.  x: [B, H, S, D] BF16/FP16/FP32 with strides; x8: contiguous
+ * [B, H, S, D] bytes; descale: [B, H] fp32.
+ */
+size_t dtattn_fp8_quantize_workspace_size(int64_t B, int64_t H, int64_t S, int64_t D);
+int dtattn_fp8_quantize_per_head(const void* x, int32_t x_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                                 const int64_t x_stride[3], void* x8, float* descale, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* Peak table of the device (analog of dtorch/external/device/device_peak_performance.cc:125-200):
+ * CU count and max engine clock from hipGetDeviceProperties times the CDNA4 per-CU dense rates
+ * (bf16/fp16 4096, fp8 8192 FLOP/clk/CU), HBM3E bandwidth 8.0e12 B/s. */
+typedef struct {
+    int32_t cu_count;
+    double clock_hz;
+    double bf16_flops;
+    double fp8_flops;
+    double hbm_bytes_per_s;
+    char arch[64];
+} dtattn_device_peaks;
+
+int dtattn_get_device_peaks(int32_t device, dtattn_device_peaks* out);
+
+const char* dtattn_last_error(void);
+int dtattn_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DTATTN_H_ */

@@ -1,0 +1,191 @@
+"""GPU parity of split-KV decode, the LSE merge and the ring-attention step against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sdpa as orc
+from tests.attn_cases import LSE_TOL, O_TOL_BF16, host, lse_rel, max_abs, randn, rounded, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _F():
+    import dtorch_amd.nn.functional as F
+    return F
+
+
+def _decode_case(B, Hq, Hkv, Smax, D, lengths, chunk=0, dtype=torch.bfloat16, seed=0, nan_pad=True):
+    rng = np.random.default_rng(seed)
+    q = randn(rng, (B, Hq, 1, D))
+    kc = randn(rng, (B, Hkv, Smax, D))
+    vc = randn(rng, (B, Hkv, Smax, D))
+    lengths = np.asarray(lengths, dtype=np.int32)
+    tk, tv = to_dev(kc, dtype), to_dev(vc, dtype)
+    if nan_pad:  # padding rows must never be read
+        for b, L in enumerate(lengths):
+            tk[b, :, L:] = float("nan")
+            tv[b, :, L:] = float("nan")
+    F = _F()
+    o, lse = F.decode_attention(to_dev(q, dtype), tk, tv, torch.from_numpy(lengths).cuda(), chunk=chunk)
+    torch.cuda.synchronize()
+    ro, rl = orc.decode(rounded(q, dtype), rounded(kc, dtype), rounded(vc, dtype), lengths)
+    return host(o), host(lse), ro, rl
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Smax,D,lengths,chunk", [
+    (3, 32, 8, 1024, 128, [1, 256, 1024], 0),
+    (4, 8, 8, 600, 128, [255, 257, 511, 600], 0),    # MHA, chunk boundaries
+    (2, 16, 2, 700, 128, [700, 129], 64),             # GQA 8
+    (2, 12, 2, 300, 128, [300, 77], 0),               # GQA 6 -> subgroups of 2
+    (2, 8, 4, 520, 64, [519, 3], 512),                # D = 64, chunk 512
+])
+def test_decode_small(B, Hq, Hkv, Smax, D, lengths, chunk):
+    o, lse, ro, rl = _decode_case(B, Hq, Hkv, Smax, D, lengths, chunk)
+    assert max_abs(o, ro) <= O_TOL_BF16
+    assert lse_rel(lse, rl) <= LSE_TOL
+
+
+def test_decode_fp16():
+    o, lse, ro, rl = _decode_case(2, 8, 2, 400, 128, [400, 33], dtype=torch.float16, seed=2)
+    assert max_abs(o, ro) <= O_TOL_BF16
+    assert lse_rel(lse, rl) <= LSE_TOL
+
+
+def test_decode_split_invariance_and_prefill_equality():
+    rng = np.random.default_rng(3)
+    B, Hq, Hkv, Smax, D = 2, 8, 2, 900, 128
+    q, kc, vc = to_dev(randn(rng, (B, Hq, 1, D))), to_dev(randn(rng, (B, Hkv, Smax, D))), to_dev(
+        randn(rng, (B, Hkv, Smax, D)))
+    lengths = torch.tensor([900, 450], dtype=torch.int32, device="cuda")
+    F = _F()
+    outs = [F.decode_attention(q, kc, vc, lengths, chunk=c) for c in (64, 128, 256, 512)]
+    for o, l in outs[1:]:
+        assert max_abs(host(o), host(outs[0][0])) <= O_TOL_BF16
+        assert lse_rel(host(l), host(outs[0][1])) <= LSE_TOL
+    for b in range(B):
+        L = int(lengths[b])
+        po, pl = F.scaled_dot_product_attention_with_lse(q[b:b + 1], kc[b:b + 1, :, :L], vc[b:b + 1, :, :L],
+                                                         enable_gqa=True)
+        assert max_abs(host(outs[2][0][b:b + 1]), host(po)) <= O_TOL_BF16
+        assert lse_rel(host(outs[2][1][b:b + 1]), host(pl)[..., 0]) <= LSE_TOL
+
+
+def test_config3_decode_full_size():
+    # B=64, Hq=32, Hkv=8, D=128, cache padded to 8192, lengths ~ U[512, 8192] drawn after Q, K, V
+    rng = np.random.default_rng(0)
+    B, Hq, Hkv, Smax, D = 64, 32, 8, 8192, 128
+    q = randn(rng, (B, Hq, 1, D))
+    kc = randn(rng, (B, Hkv, Smax, D))
+    vc = randn(rng, (B, Hkv, Smax, D))
+    lengths = rng.integers(512, 8192, size=B, endpoint=True).astype(np.int32)
+    tk, tv = to_dev(kc), to_dev(vc)
+    del kc, vc
+    F = _F()
+    o, lse = F.decode_attention(to_dev(q), tk, tv, torch.from_numpy(lengths).cuda())
+    torch.cuda.synchronize()
+    o, lse = host(o), host(lse)
+    kb = tk.float().cpu().numpy()
+    vb = tv.float().cpu().numpy()
+    ro, rl = orc.decode(rounded(q), kb, vb, lengths)
+    assert max_abs(o, ro) <= O_TOL_BF16
+    assert lse_rel(lse, rl) <= LSE_TOL
+
+
+# --------------------------------------------------------------------------- merge
+
+@pytest.mark.parametrize("n,dtype", [(1, torch.bfloat16), (2, torch.bfloat16), (3, torch.float32),
+                                     (4, torch.bfloat16), (16, torch.float16)])
+def test_merge_random_blocks(n, dtype):
+    rng = np.random.default_rng(n)
+    B, H, S, D = 2, 4, 77, 128
+    os_ = [randn(rng, (B, H, S, D)) for _ in range(n)]
+    ls_ = [randn(rng, (B, H, S)) * 3 for _ in range(n)]
+    F = _F()
+    o, lse = F.lse_merge([to_dev(x, dtype) for x in os_], [torch.from_numpy(x).cuda() for x in ls_])
+    ro, rl = orc.lse_merge([rounded(x, dtype) for x in os_], ls_)
+    tol = 1e-5 if dtype == torch.float32 else O_TOL_BF16
+    assert max_abs(host(o), ro) <= tol
+    assert lse_rel(host(lse), rl) <= 1e-6
+
+
+def test_merge_identity_and_neg_inf_block():
+    rng = np.random.default_rng(9)
+    o0 = to_dev(randn(rng, (1, 2, 64, 128)))
+    l0 = torch.from_numpy(randn(rng, (1, 2, 64))).cuda()
+    F = _F()
+    o, l = F.lse_merge([o0], [l0])
+    assert torch.equal(o, o0)
+    assert torch.allclose(l, l0, atol=1e-6, rtol=0)
+    junk = torch.full_like(o0, float("nan"))
+    o2, l2 = F.lse_merge([o0, junk], [l0, torch.full_like(l0, float("-inf"))])
+    assert torch.equal(o2, o0)
+    assert torch.allclose(l2, l0, atol=1e-6, rtol=0)
+
+
+def test_merge_of_kv_splits_equals_single_pass():
+    rng = np.random.default_rng(10)
+    q, k, v = to_dev(randn(rng, (1, 4, 200, 128))), to_dev(randn(rng, (1, 4, 700, 128))), to_dev(
+        randn(rng, (1, 4, 700, 128)))
+    F = _F()
+    ref_o, ref_l = F.scaled_dot_product_attention_with_lse(q, k, v)
+    cuts = [0, 64, 300, 301, 700]
+    parts = [F.scaled_dot_product_attention_with_lse(q, k[:, :, a:b].contiguous(), v[:, :, a:b].contiguous())
+             for a, b in zip(cuts[:-1], cuts[1:])]
+    o, l = F.lse_merge([p[0] for p in parts], [p[1] for p in parts])
+    assert max_abs(host(o), host(ref_o)) <= O_TOL_BF16
+    assert lse_rel(host(l), host(ref_l)) <= LSE_TOL
+
+
+# --------------------------------------------------------------------------- ring step
+
+def test_ring_step_small_all_ranks():
+    rng = np.random.default_rng(11)
+    n, C, Hq, Hkv, D = 4, 96, 8, 2, 128
+    q_all = randn(rng, (1, Hq, n * C, D))
+    k_all = randn(rng, (1, Hkv, n * C, D))
+    v_all = randn(rng, (1, Hkv, n * C, D))
+    ro, rl = orc.sdpa_fwd(rounded(q_all), rounded(k_all), rounded(v_all), is_causal=True, enable_gqa=True)
+    F = _F()
+    kch = [to_dev(k_all[:, :, i * C:(i + 1) * C]) for i in range(n)]
+    vch = [to_dev(v_all[:, :, i * C:(i + 1) * C]) for i in range(n)]
+    for idx in range(n):
+        o, l = F.ring_attention_step(to_dev(q_all[:, :, idx * C:(idx + 1) * C]), kch, vch, idx)
+        assert max_abs(host(o), ro[:, :, idx * C:(idx + 1) * C]) <= O_TOL_BF16
+        assert lse_rel(host(l), rl[:, :, idx * C:(idx + 1) * C]) <= LSE_TOL
+
+
+def test_config4_ring_step_full_size():
+    # Q chunk of 4096 tokens (global chunk 3) against 4 KV chunks of 4096: 1 causal diagonal + 3 full,
+    # Hq=32, Hkv=8, D=128, B=1, bf16; checked on sampled heads and rows against the single pass over
+    # all 16384 keys.
+    rng = np.random.default_rng(0)
+    C, Hq, Hkv, D = 4096, 32, 8, 128
+    q = randn(rng, (1, Hq, C, D))
+    k = [randn(rng, (1, Hkv, C, D)) for _ in range(4)]
+    v = [randn(rng, (1, Hkv, C, D)) for _ in range(4)]
+    F = _F()
+    o, l, blocks = F.ring_attention_step(to_dev(q), [to_dev(x) for x in k], [to_dev(x) for x in v], 3,
+                                         return_blocks=True)
+    torch.cuda.synchronize()
+    assert len(blocks) == 4
+    k_all = np.concatenate(k, axis=2)
+    v_all = np.concatenate(v, axis=2)
+    rows = np.r_[0:64, 2000:2064, 4032:4096]
+    for h in (0, 17, 31):
+        hk = h // 4
+        qs = rounded(q[0, h, rows])[None]
+        # global query position = 3*C + row; keys 0..16383 under the causal rule
+        ro, rl = _causal_rows(qs[0], rounded(k_all[0, hk]), rounded(v_all[0, hk]), 3 * C + rows)
+        assert max_abs(host(o[0, h, rows]), ro) <= O_TOL_BF16, h
+        assert lse_rel(host(l[0, h, rows]), rl) <= LSE_TOL, h
+
+
+def _causal_rows(q, k, v, qpos):
+    scale = 1 / np.sqrt(q.shape[-1])
+    logits = (q @ k.T) * scale
+    keep = np.arange(k.shape[0])[None, :] <= qpos[:, None]
+    logits = np.where(keep, logits, -np.inf)
+    m = logits.max(-1, keepdims=True)
+    p = np.exp(logits - m)
+    s = p.sum(-1, keepdims=True)
+    return (p @ v) / s, (m + np.log(s))[:, 0]

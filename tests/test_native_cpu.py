@@ -1,0 +1,207 @@
+"""CPU-only checks of the native library and host operators (no kernel is launched).
+
+* libdtattn.so loads and exports every function include/dtattn.h declares;
+* the C ABI rejects bad arguments before touching a device, with the documented status codes and a
+  readable dtattn_last_error();
+* the SdpaOp mirror reproduces the reference's shape inference, placement signature and cost
+  (scaled_dot_product_attention_op.cc:16-95, dtorch/tests/test_operator_cost.cc:171-183);
+* errors surface as the reference's exception type (std::invalid_argument -> ValueError).
+"""
+import ctypes
+import os
+import pickle
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dtattn.h")
+
+from dtorch_amd import _lib  # noqa: E402
+
+lib = _lib.cabi()
+host = _lib.load()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\**\s+\**(dtattn_[a-z_0-9]+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    for n in ["dtattn_prefill_fwd", "dtattn_decode_splitkv", "dtattn_decode_workspace_size", "dtattn_lse_merge",
+              "dtattn_fp8_quantize_per_head", "dtattn_fp8_quantize_workspace_size", "dtattn_get_device_peaks",
+              "dtattn_last_error", "dtattn_abi_version"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_abi_version_matches_header():
+    ver = int(re.search(r"#define DTATTN_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    lib.dtattn_abi_version.restype = ctypes.c_int
+    assert lib.dtattn_abi_version() == ver == host.abi_version()
+
+
+# ---- ctypes mirror of dtattn_prefill_args (only used for validation paths)
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("o", ctypes.c_void_p),
+                ("lse", ctypes.c_void_p),
+                ("B", ctypes.c_int64), ("Hq", ctypes.c_int64), ("Hkv", ctypes.c_int64), ("Sq", ctypes.c_int64),
+                ("Sk", ctypes.c_int64), ("D", ctypes.c_int64), ("Dv", ctypes.c_int64),
+                ("q_stride", ctypes.c_int64 * 3), ("k_stride", ctypes.c_int64 * 3), ("v_stride", ctypes.c_int64 * 3),
+                ("o_stride", ctypes.c_int64 * 3), ("lse_stride", ctypes.c_int64 * 2),
+                ("dtype", ctypes.c_int32), ("o_dtype", ctypes.c_int32), ("scale", ctypes.c_float),
+                ("causal", ctypes.c_int32), ("q_offset", ctypes.c_int64), ("k_offset", ctypes.c_int64),
+                ("q_descale", ctypes.c_void_p), ("k_descale", ctypes.c_void_p), ("v_descale", ctypes.c_void_p)]
+
+
+def _args(**kw):
+    a = PrefillArgs()
+    fake = 0x10000  # never dereferenced: every case below fails validation first
+    a.q = a.k = a.v = a.o = fake
+    a.B, a.Hq, a.Hkv, a.Sq, a.Sk, a.D, a.Dv = 1, 8, 8, 64, 64, 128, 128
+    for s in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
+        s[0], s[1], s[2] = 8 * 64 * 128, 64 * 128, 128
+    a.dtype = a.o_dtype = 0
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _last_error():
+    lib.dtattn_last_error.restype = ctypes.c_char_p
+    return lib.dtattn_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,text", [
+    (dict(Hq=6, Hkv=4), 1, "multiple"),
+    (dict(D=96, Dv=96), 2, "head dim"),
+    (dict(Dv=64), 2, "Dv"),
+    (dict(dtype=3, o_dtype=3), 2, "dtype"),
+    (dict(dtype=2, o_dtype=0), 1, "descale"),
+    (dict(q=0), 1, "null"),
+    (dict(Sq=-1), 1, "bad sizes"),
+])
+def test_prefill_validation(kw, code, text):
+    lib.dtattn_prefill_fwd.restype = ctypes.c_int
+    a = _args(**kw)
+    assert lib.dtattn_prefill_fwd(ctypes.byref(a), None) == code
+    assert text in _last_error()
+
+
+def test_prefill_null_args():
+    assert lib.dtattn_prefill_fwd(None, None) == 1
+    assert "NULL" in _last_error()
+
+
+def test_empty_problem_is_a_no_op():
+    assert lib.dtattn_prefill_fwd(ctypes.byref(_args(B=0)), None) == 0
+
+
+def test_workspace_sizes():
+    lib.dtattn_decode_workspace_size.restype = ctypes.c_size_t
+    lib.dtattn_decode_workspace_size.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_int32]
+    n = lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 256)
+    nsplit = 8192 // 256
+    o_bytes = 64 * 32 * nsplit * 128 * 4
+    lse_bytes = 64 * 32 * nsplit * 4
+    assert n == o_bytes + ((lse_bytes + 255) // 256) * 256
+    assert lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 0) == n  # default chunk 256
+    lib.dtattn_fp8_quantize_workspace_size.restype = ctypes.c_size_t
+    lib.dtattn_fp8_quantize_workspace_size.argtypes = [ctypes.c_int64] * 4
+    assert lib.dtattn_fp8_quantize_workspace_size(1, 24, 4608, 128) == ((24 * 18 * 4 + 255) // 256) * 256
+
+
+def test_merge_validation():
+    class MergeArgs(ctypes.Structure):
+        _fields_ = [("n_blocks", ctypes.c_int32), ("o_blocks", ctypes.c_void_p * 16),
+                    ("lse_blocks", ctypes.c_void_p * 16), ("B", ctypes.c_int64), ("H", ctypes.c_int64),
+                    ("S", ctypes.c_int64), ("D", ctypes.c_int64), ("block_o_stride", ctypes.c_int64 * 3),
+                    ("block_lse_stride", ctypes.c_int64 * 2), ("block_dtype", ctypes.c_int32),
+                    ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p), ("o_stride", ctypes.c_int64 * 3),
+                    ("lse_stride", ctypes.c_int64 * 2), ("o_dtype", ctypes.c_int32)]
+    a = MergeArgs()
+    a.n_blocks = 17
+    assert lib.dtattn_lse_merge(ctypes.byref(a), None) == 1 and "n_blocks" in _last_error()
+    a.n_blocks, a.B, a.H, a.S, a.D = 2, 1, 1, 4, 128
+    a.o = 0x10000
+    for s in (a.block_o_stride, a.o_stride):
+        s[0], s[1], s[2] = 512, 512, 128
+    a.o_blocks[0] = 0x10000
+    assert lib.dtattn_lse_merge(ctypes.byref(a), None) == 1 and "null" in _last_error()
+
+
+# --------------------------------------------------------------------------- host operator metadata
+
+def test_infer_output_meta_info():
+    op = host.SdpaOp(host.SdpaParam())
+    assert op.infer_output_meta_info([1, 8, 512, 64], [1, 8, 512, 64], [1, 8, 512, 32]) == [1, 8, 512, 32]
+    assert op.infer_output_meta_info([2, 3, 4, 32, 7, 16], [2, 3, 4, 32, 9, 16], [2, 3, 4, 32, 9, 16]) == \
+        [2, 3, 4, 32, 7, 16]
+    with pytest.raises(ValueError):
+        op.infer_output_meta_info([8, 512, 64], [8, 512, 64], [8, 512, 64])
+
+
+def test_operator_cost_matches_reference_test():
+    op = host.SdpaOp(host.SdpaParam())
+    assert op.get_operator_cost([2, 8, 16, 64], [2, 8, 20, 64], [2, 8, 20, 64]) == 2 * 2 * 8 * 16 * 20 * (64 + 64)
+    # rank 5: batch = Prod(0, NumAxis - 4) over an inclusive range
+    assert op.get_operator_cost([3, 2, 8, 16, 64], [3, 2, 8, 20, 64], [3, 2, 8, 20, 64]) == \
+        2 * 6 * 8 * 16 * 20 * 128
+    causal = host.SdpaOp(host.SdpaParam(True, None, False, None))
+    assert causal.get_algorithmic_flops([4, 32, 2048, 128], [4, 8, 2048, 128], [4, 8, 2048, 128]) == 137506062336
+    assert causal.get_operator_cost([4, 32, 2048, 128], [4, 8, 2048, 128], [4, 8, 2048, 128]) == 274877906944
+
+
+def test_placement_signature_matches_reference():
+    # scaled_dot_product_attention_op.cc:34-66 plus placement_signature.cc:65-88 (all-Replicate)
+    op = host.SdpaOp(host.SdpaParam())
+    rules = [(r.inputs, r.outputs) for r in op.get_placement_signature(4)]
+    assert rules == [
+        (["S(0)", "S(0)", "S(0)", "S(0)"], ["S(0)"]),
+        (["S(1)", "S(1)", "S(1)", "R"], ["S(1)"]),
+        (["S(2)", "R", "R", "R"], ["S(2)"]),
+        (["R", "R", "R", "R"], ["R"]),
+    ]
+    assert len(op.get_placement_signature(5)) == 5  # heads axes 1 and 2 for rank 5
+    assert op.match_placements(4, ["S(1)", "S(1)", "S(1)", ""]) == ["S(1)"]
+    assert op.match_placements(4, ["S(2)", "R", "R", ""]) == ["S(2)"]
+    with pytest.raises(ValueError):
+        op.match_placements(4, ["S(2)", "S(2)", "S(2)", ""])  # ring needs K/V replicated
+
+
+def test_param_serialisation_round_trip():
+    p = host.SdpaParam(True, 0.125, True, host.SdpaOption("native_fp8"))
+    q = pickle.loads(pickle.dumps(p))
+    assert (q.is_causal, q.scale, q.enable_gqa, q.option.sage_attention_type) == (True, 0.125, True, "native_fp8")
+    d = pickle.loads(pickle.dumps(host.SdpaParam()))
+    assert (d.is_causal, d.scale, d.enable_gqa, d.option) == (False, None, False, None)
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    import dtorch_amd.nn.functional as F
+    x = torch.randn(1, 2, 8, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="device tensors"):
+        F.scaled_dot_product_attention(x, x, x)
+    with pytest.raises(ValueError, match="device tensors"):
+        F.lse_merge([x], [torch.zeros(1, 2, 8)])
+
+
+def test_front_end_option_validation():
+    import dtorch_amd.nn.functional as F
+    assert F.SdpaOption().check_valid()
+    assert F.SdpaOption(sage_attn_type="native_fp8").check_valid()
+    assert not F.SdpaOption(sage_attn_type="int4").check_valid()
+    x = torch.randn(1, 2, 8, 64)
+    with pytest.raises(AssertionError):
+        F.scaled_dot_product_attention(x, x, x, sdpa_option=F.SdpaOption(sage_attn_type="int4"))
+    with pytest.raises(RuntimeError, match="sageattention"):
+        F.scaled_dot_product_attention(x, x, x, sdpa_option=F.SdpaOption(sage_attn_type="auto"))
+    with pytest.raises(NotImplementedError):
+        F.scaled_dot_product_attention(x, x, x, sdpa_option=F.SdpaOption(ring_cp_dim=2))
