@@ -38,7 +38,6 @@ struct DecodeParams {
 };
 
 constexpr int kDecodeChunk = 256;
-constexpr int kMaxChunk = 512;
 
 size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk, int64_t* nsplit_out) {
     const int64_t nsplit = (S_max + chunk - 1) / chunk;
@@ -48,14 +47,25 @@ size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t 
     return ((o_bytes + 255) & ~(size_t)255) + ((lse_bytes + 255) & ~(size_t)255);
 }
 
-// G heads per workgroup, D head dim, C tokens per chunk (4 waves x C/4 tokens).
-template <typename T, int D, int G>
+// G heads per workgroup, D head dim, TPW tokens per wave (chunk = 4 * TPW).  A wave walks its
+// tokens in sub-blocks of SB = min(TPW, 64) tokens; all loops have compile-time trip counts, so the
+// K and V loads of a sub-block are issued together (and the compiler may hoist the next sub-block's).
+// Loads go through a buffer resource over the chunk's valid rows: rows past the sequence read zeros
+// without a branch.  A token row is read by D/8 lanes (one DPP row for D = 128), so the score is a
+// v_dot2 chain plus a DPP row sum; the chunk softmax is online per wave, and the 4 waves combine once
+// through LDS.
+template <typename T, int D, int G, int TPW>
 __global__ void __launch_bounds__(256) decode_partial_kernel(const DecodeParams p) {
-    constexpr int LPT = D / 8;          // lanes per token row
-    constexpr int TPI = 64 / LPT;       // tokens per wave-wide load
-    __shared__ float sc[G][kMaxChunk];  // scores, then probabilities
-    __shared__ float red[4][G][D];      // per-wave partial P V
-    __shared__ float stat[G][2];        // max (log2 domain), sum
+    constexpr int LPT = D / 8;            // lanes per token row
+    constexpr int TPI = 64 / LPT;         // tokens per wave-wide load
+    constexpr int SB = TPW < 64 ? TPW : 64;
+    constexpr int NSB = TPW / SB;         // sub-blocks per wave
+    constexpr int NI = SB / TPI;          // K (and V) loads per lane per sub-block
+    constexpr int C = 4 * TPW;
+    static_assert(NI >= 1 && TPW % SB == 0, "bad chunk");
+    __shared__ float red_o[4][G][D];
+    __shared__ float red_m[4][G];
+    __shared__ float red_l[4][G];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -65,131 +75,132 @@ __global__ void __launch_bounds__(256) decode_partial_kernel(const DecodeParams 
     const int sg = blockIdx.y / p.Hkv;   // head subgroup within the kv group
     const int b = blockIdx.z;
     const int L = min(max(p.lengths[b], 0), p.S_max);  // never read past the cache
-    const int C = p.chunk;
     const int t0 = split * C;
     if (t0 >= L) return;
     const int n_tok = min(C, L - t0);
-    const int tpw = C / 4;               // tokens per wave
-    const int NI = tpw / TPI;            // loads per wave
-
     const int hq0 = hk * p.group + sg * G;
     const int c8 = lane % LPT;           // 16-byte chunk of the row this lane reads
     const int tsub = lane / LPT;
 
-    // q chunks for the G heads (packed pairs for v_dot2).
     u32x4 qv[G];
 #pragma unroll
     for (int g = 0; g < G; ++g)
         qv[g] = ld16(reinterpret_cast<const T*>(p.q) + b * p.qs_b + (hq0 + g) * p.qs_h + c8 * 8);
 
-    const T* kp = reinterpret_cast<const T*>(p.k) + b * p.ks_b + hk * p.ks_h;
-    const T* vp = reinterpret_cast<const T*>(p.v) + b * p.vs_b + hk * p.vs_h;
+    const int kpitch = (int)(p.ks_s * (int64_t)sizeof(T));
+    const int vpitch = (int)(p.vs_s * (int64_t)sizeof(T));
+    const T* kp = reinterpret_cast<const T*>(p.k) + b * p.ks_b + hk * p.ks_h + (int64_t)t0 * p.ks_s;
+    const T* vp = reinterpret_cast<const T*>(p.v) + b * p.vs_b + hk * p.vs_h + (int64_t)t0 * p.vs_s;
+    const auto krs = make_rsrc(kp, (uint32_t)((n_tok - 1) * kpitch + D * (int)sizeof(T)));
+    const auto vrs = make_rsrc(vp, (uint32_t)((n_tok - 1) * vpitch + D * (int)sizeof(T)));
 
-    // ---- scores
-    for (int i0 = 0; i0 < NI; i0 += 8) {
-        u32x4 kr[8];
+    float m[G], l[G], acc[G][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int tl = wave * tpw + (i0 + j) * TPI + tsub;
-            kr[j] = u32x4{0u, 0u, 0u, 0u};
-            if (i0 + j < NI && tl < n_tok) kr[j] = ld16(kp + (int64_t)(t0 + tl) * p.ks_s + c8 * 8);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (i0 + j >= NI) break;
-            const int tl = wave * tpw + (i0 + j) * TPI + tsub;
-            float sg_[G];
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float acc = 0.f;
-                acc = Elem<T>::dot2(kr[j].x, qv[g].x, acc);
-                acc = Elem<T>::dot2(kr[j].y, qv[g].y, acc);
-                acc = Elem<T>::dot2(kr[j].z, qv[g].z, acc);
-                acc = Elem<T>::dot2(kr[j].w, qv[g].w, acc);
-#pragma unroll
-                for (int m = 1; m < LPT; m <<= 1) acc += shfl_xor_f(acc, m);
-                sg_[g] = acc;
-            }
-            if (c8 == 0 && tl < C) {
-#pragma unroll
-                for (int g = 0; g < G; ++g) sc[g][tl] = tl < n_tok ? sg_[g] * p.c : kNegInf;
-            }
-        }
-    }
-    __syncthreads();
-
-    // ---- softmax over the chunk (log2 domain), one wave per head (round robin)
-    for (int g = wave; g < G; g += 4) {
-        float mx = kNegInf;
-        for (int t = lane; t < C; t += 64) mx = fmaxf(mx, sc[g][t]);
-        mx = wave_max(mx);
-        float sum = 0.f;
-        for (int t = lane; t < C; t += 64) {
-            const float e = fast_exp2(sc[g][t] - mx);
-            sc[g][t] = e;
-            sum += e;
-        }
-        sum = wave_sum(sum);
-        if (lane == 0) {
-            stat[g][0] = mx;
-            stat[g][1] = sum;
-        }
-    }
-    __syncthreads();
-
-    // ---- P V
-    float acc[G][8];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g) {
+        m[g] = kNegInf;
+        l[g] = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-    for (int i0 = 0; i0 < NI; i0 += 8) {
-        u32x4 vr[8];
+    }
+
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int tl = wave * tpw + (i0 + j) * TPI + tsub;
-            vr[j] = u32x4{0u, 0u, 0u, 0u};
-            if (i0 + j < NI && tl < n_tok) vr[j] = ld16(vp + (int64_t)(t0 + tl) * p.vs_s + c8 * 8);
+    for (int sb = 0; sb < NSB; ++sb) {
+        u32x4 kr[NI], vr[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int tl = wave * TPW + sb * SB + i * TPI + tsub;
+            kr[i] = buf_ld16(krs, (uint32_t)(tl * kpitch + c8 * 16));
+            vr[i] = buf_ld16(vrs, (uint32_t)(tl * vpitch + c8 * 16));
         }
+        float sc[NI][G];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (i0 + j >= NI) break;
-            const int tl = wave * tpw + (i0 + j) * TPI + tsub;
-            if (tl >= n_tok) continue;
-            float vf[8];
-            unpack8<T>(vr[j], vf);
+        for (int i = 0; i < NI; ++i) {
+            const bool ok = wave * TPW + sb * SB + i * TPI + tsub < n_tok;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float pw = sc[g][tl];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] = __builtin_fmaf(pw, vf[e], acc[g][e]);
+                float a = 0.f;
+                a = Elem<T>::dot2(kr[i].x, qv[g].x, a);
+                a = Elem<T>::dot2(kr[i].y, qv[g].y, a);
+                a = Elem<T>::dot2(kr[i].z, qv[g].z, a);
+                a = Elem<T>::dot2(kr[i].w, qv[g].w, a);
+                a = group_sum<LPT>(a);
+                sc[i][g] = ok ? a * p.c : kNegInf;
             }
         }
-    }
-    // reduce across the TPI token lanes that share a chunk, then across waves through LDS
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int g = 0; g < G; ++g) {
+            float mx = kNegInf;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) mx = fmaxf(mx, sc[i][g]);
+#pragma unroll
+            for (int mk = LPT; mk < 64; mk <<= 1) mx = fmaxf(mx, shfl_xor_f(mx, mk));
+            const float mnew = fmaxf(m[g], mx);
+            const float mbase = mnew == kNegInf ? 0.f : mnew;
+            const float alpha = fast_exp2(m[g] - mbase);
+            m[g] = mnew;
+            float ls = l[g] * alpha;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const float pw = fast_exp2(sc[i][g] - mbase);
+                sc[i][g] = pw;
+                ls += pw;
+            }
+            l[g] = ls;
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            float vf[8];
+            unpack8<T>(vr[i], vf);
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] = __builtin_fmaf(sc[i][g], vf[e], acc[g][e]);
+        }
+    }
+    // reduce across the TPI token lanes of each row position (same c8), then across waves
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int mk = LPT; mk < 64; mk <<= 1) l[g] += shfl_xor_f(l[g], mk);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             float x = acc[g][e];
 #pragma unroll
-            for (int m = LPT; m < 64; m <<= 1) x += shfl_xor_f(x, m);
+            for (int mk = LPT; mk < 64; mk <<= 1) x += shfl_xor_f(x, mk);
             acc[g][e] = x;
         }
+    }
     if (tsub == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) red[wave][g][c8 * 8 + e] = acc[g][e];
+            for (int e = 0; e < 8; ++e) red_o[wave][g][c8 * 8 + e] = acc[g][e];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            red_m[wave][g] = m[g];
+            red_l[wave][g] = l[g];
+        }
     }
     __syncthreads();
     for (int idx = tid; idx < G * D; idx += 256) {
         const int g = idx / D, d = idx % D;
-        const float sum = stat[g][1];
-        const float val = (red[0][g][d] + red[1][g][d] + red[2][g][d] + red[3][g][d]) / sum;
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][g]);
+        float Lsum = 0.f, val = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float f = red_m[w][g] == kNegInf ? 0.f : fast_exp2(red_m[w][g] - M);
+            Lsum += f * red_l[w][g];
+            val += f * red_o[w][g][d];
+        }
         const int hq = hq0 + g;
-        p.part_o[(((int64_t)b * p.Hq + hq) * p.nsplit + split) * D + d] = val;
-        if (d == 0) p.part_lse[((int64_t)b * p.Hq + hq) * p.nsplit + split] = (stat[g][0] + __log2f(sum)) * kLn2;
+        p.part_o[(((int64_t)b * p.Hq + hq) * p.nsplit + split) * D + d] = val / Lsum;
+        if (d == 0) p.part_lse[((int64_t)b * p.Hq + hq) * p.nsplit + split] = (M + __log2f(Lsum)) * kLn2;
     }
 }
 
@@ -232,10 +243,10 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p)
     if (p.lse != nullptr && lane == 0) p.lse[b * p.lses_b + hq] = mx + __logf(sum);
 }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, int TPW>
 static int launch_decode(const DecodeParams& p, hipStream_t stream) {
     dim3 grid1((unsigned)p.nsplit, (unsigned)(p.Hkv * (p.group / G)), (unsigned)p.B);
-    hipLaunchKernelGGL((decode_partial_kernel<T, D, G>), grid1, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_partial_kernel<T, D, G, TPW>), grid1, dim3(256), 0, stream, p);
     int st = check_launch("decode_partial_kernel");
     if (st != DTATTN_OK) return st;
     const int64_t pairs = (int64_t)p.B * p.Hq;
@@ -243,13 +254,23 @@ static int launch_decode(const DecodeParams& p, hipStream_t stream) {
     return check_launch("decode_merge_kernel");
 }
 
+template <typename T, int D, int G>
+static int dispatch_chunk(const DecodeParams& p, hipStream_t stream) {
+    switch (p.chunk) {
+        case 128: return launch_decode<T, D, G, 32>(p, stream);
+        case 256: return launch_decode<T, D, G, 64>(p, stream);
+        case 512: return launch_decode<T, D, G, 128>(p, stream);
+        default: return fail(DTATTN_ERR_UNSUPPORTED, "decode: chunk %d not supported (128, 256, 512)", p.chunk);
+    }
+}
+
 template <typename T, int D>
 static int dispatch_group(const DecodeParams& p, hipStream_t stream) {
     const int g = p.group;
-    if (g % 8 == 0) return launch_decode<T, D, 8>(p, stream);
-    if (g % 4 == 0) return launch_decode<T, D, 4>(p, stream);
-    if (g % 2 == 0) return launch_decode<T, D, 2>(p, stream);
-    return launch_decode<T, D, 1>(p, stream);
+    if (g % 8 == 0) return dispatch_chunk<T, D, 8>(p, stream);
+    if (g % 4 == 0) return dispatch_chunk<T, D, 4>(p, stream);
+    if (g % 2 == 0) return dispatch_chunk<T, D, 2>(p, stream);
+    return dispatch_chunk<T, D, 1>(p, stream);
 }
 
 template <typename T>
@@ -279,9 +300,11 @@ extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_)
     if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16)
         return fail(DTATTN_ERR_UNSUPPORTED, "decode: dtype %d not supported (bf16, fp16)", a->dtype);
     const int32_t chunk = a->chunk > 0 ? a->chunk : kDecodeChunk;
-    if (chunk % 64 != 0 || chunk > kMaxChunk)
-        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: chunk %d must be a multiple of 64 and <= %d", chunk,
-                    kMaxChunk);
+    if (chunk != 128 && chunk != 256 && chunk != 512)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: chunk %d must be 128, 256 or 512", chunk);
+    // chunk rows are addressed with 32-bit byte offsets
+    if (a->k_stride[2] * 2 * chunk >= ((int64_t)1 << 31) || a->v_stride[2] * 2 * chunk >= ((int64_t)1 << 31))
+        return fail(DTATTN_ERR_UNSUPPORTED, "decode: cache row pitch too large");
     if (a->q == nullptr || a->k_cache == nullptr || a->v_cache == nullptr || a->lengths == nullptr || a->o == nullptr)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: null pointer");
     const int64_t esz = 2;

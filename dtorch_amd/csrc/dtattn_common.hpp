@@ -85,6 +85,22 @@ __device__ __forceinline__ u32x4 pack8(const float* in) {
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
+// Buffer resource over `bytes` bytes from `base` (raw, stride 0).  Loads at offsets >= bytes return
+// zeros instead of touching memory, which is how tile loads handle ragged tails.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// 16-byte load through a buffer resource (voffset in bytes).
+__device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0));
+}
+
+// 16 bytes per lane straight into LDS: lane l lands at lds + 16 * l (lds is wave-uniform).
+__device__ __forceinline__ void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+}
+
 // ---- wave helpers -----------------------------------------------------------------------------
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
@@ -101,7 +117,37 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// DPP lane exchanges within a row of 16 lanes (no LDS round trip, unlike ds_bpermute).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141; // lane i <- lane 7-i within each half row
+constexpr int kDppRowMirror = 0x140;     // lane i <- lane 15-i within the row
+
+// Sum over aligned groups of N lanes (N = 8 or 16); every lane of the group receives the total.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+    static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
+    x += dpp_f<kDppQuadXor1>(x);
+    x += dpp_f<kDppQuadXor2>(x);
+    x += dpp_f<kDppRowHalfMirror>(x);
+    if (N == 16) x += dpp_f<kDppRowMirror>(x);
+    return x;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroup barrier for LDS producer/consumer hand-offs: waits only for this wave's LDS operations
+// (lgkmcnt) before s_barrier.  __syncthreads() is a workgroup release fence, which on gfx9 also
+// drains every outstanding global load (vmcnt(0)) and so would stall prefetches in flight.  The
+// memory clobber keeps the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Wait until this wave's global loads, including direct global->LDS loads, have completed.
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---- host-side status plumbing ----------------------------------------------------------------
 

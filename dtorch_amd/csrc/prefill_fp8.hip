@@ -103,8 +103,8 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
 
     int kend = p.Sk;
     if (CAUSAL) {
-        const int64_t lim = (int64_t)q0 + BM + p.delta;
-        kend = (int)(lim < 0 ? 0 : (lim < p.Sk ? lim : p.Sk));
+        const int lim = q0 + BM + p.delta;
+        kend = lim < 0 ? 0 : (lim < p.Sk ? lim : p.Sk);
     }
     const int nt = (kend + BN - 1) / BN;
 
@@ -190,13 +190,12 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
     }
 
     for (int t = 0; t < nt; ++t) {
-        __syncthreads();
+        lds_barrier();
         if (t + 1 < nt) load_k(t + 1);
 
         const int kbase = t * BN;
-        const bool wave_skip = CAUSAL && ((int64_t)kbase > (int64_t)wq0 + 31 + p.delta);
-        const bool need_mask =
-            (kbase + BN > p.Sk) || (CAUSAL && ((int64_t)kbase + BN - 1 > (int64_t)wq0 + p.delta));
+        const bool wave_skip = CAUSAL && (kbase > wq0 + 31 + p.delta);
+        const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && (kbase + BN - 1 > wq0 + p.delta));
 
         f32x16 s[KT];
         i32x8 pb;
@@ -225,16 +224,14 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
 
         if (!wave_skip) {
             if (need_mask) {
-                const int64_t qlim = (int64_t)wq0 + l32 + p.delta;
+                int lim = p.Sk - 1 - kbase;
+                if (CAUSAL) lim = min(lim, wq0 + l32 + p.delta - kbase);
+                lim -= 4 * hf;
 #pragma unroll
                 for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int key = kbase + kt * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
-                        bool vis = key < p.Sk;
-                        if (CAUSAL) vis = vis && ((int64_t)key <= qlim);
-                        if (!vis) s[kt][i] = kNegInf;
-                    }
+                    for (int i = 0; i < 16; ++i)
+                        if (kt * 32 + 8 * (i >> 2) + (i & 3) > lim) s[kt][i] = kNegInf;
             }
             float mx = kNegInf;
 #pragma unroll
@@ -270,7 +267,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
             lrow = ls;
         }
 
-        __syncthreads();
+        lds_barrier();
         if (t + 1 < nt) {
             store_k();
             load_v(t + 1);

@@ -21,9 +21,10 @@
 //   K  tile: [64 keys][D], 16-byte chunk c of row r stored at chunk c ^ kswz(r).
 //   V^T tile: [D][64 keys], 4-key group g of row d stored at group g ^ ((d & 15) ^ ((d >> 4) & 15)).
 //
-// Pipeline per key tile j (one LDS buffer each for K and V^T, register prefetch one tile ahead):
-//   barrier | prefetch K[j+1] -> regs | S = K[j] Q^T | V[j] regs -> LDS | softmax |
-//   barrier | K[j+1] regs -> LDS | prefetch V[j+1] -> regs | O^T += V^T P^T
+// Pipeline per key tile j (K double-buffered in LDS and filled by direct global->LDS loads, V
+// prefetched one tile ahead in registers and transposed into a single V^T buffer):
+//   wait + barrier | V[j] regs -> V^T | V[j+1] -> regs (async) | K[j+1] -> LDS (async) |
+//   S = K[j] Q^T | softmax | barrier | O^T += V^T P^T
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -70,19 +71,17 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     constexpr int DT = D / 32;            // 32-row d tiles of O^T
     constexpr int KT = BN / 32;           // 32-key tiles per key block
     constexpr int PVS = BN / 16;          // MFMA k-steps of O^T = V^T P^T
-    constexpr int KPT = BN * DCH / 256;   // K chunks per thread
     constexpr int NVB = (BN / 4) * DCH;   // 4-key x 8-d blocks of V per tile
-    constexpr int OSTR = D + 8;           // staging row stride (elements)
-    constexpr int KV_BYTES = 2 * BN * D * 2;
-    constexpr int O_BYTES = NW * QT * 32 * OSTR * 2;
-    constexpr int SMEM = KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES;
-    static_assert(KPT >= 1 && (BN * DCH) % 256 == 0, "tile/thread mismatch");
+    static_assert((BN * DCH) % 256 == 0, "tile/thread mismatch");
     static_assert(NVB <= 256, "one V block per thread at most");
+    static_assert(QT == 1, "the output staging reuses the two K buffers: 2 waves x 32 rows each");
     typedef typename Elem<T>::vec8 V8;
 
-    __shared__ __attribute__((aligned(16))) char smem[SMEM];
-    T* Ks = reinterpret_cast<T*>(smem);
-    T* VTs = Ks + BN * D;
+    // Three distinct LDS objects so the compiler's alias analysis can tell the in-flight K load
+    // (into one buffer) from the reads of the other buffer and from the V^T writes.
+    __shared__ __attribute__((aligned(16))) T Ksa[BN * D];
+    __shared__ __attribute__((aligned(16))) T Ksb[BN * D];
+    __shared__ __attribute__((aligned(16))) T VTs[D * BN];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -107,8 +106,8 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
 
     int kend = p.Sk;
     if (CAUSAL) {
-        const int64_t lim = (int64_t)q0 + BM + p.delta;  // keys < lim can be visible
-        kend = (int)(lim < 0 ? 0 : (lim < p.Sk ? lim : p.Sk));
+        const int lim = q0 + BM + p.delta;  // keys < lim can be visible
+        kend = lim < 0 ? 0 : (lim < p.Sk ? lim : p.Sk);
     }
     const int nt = (kend + BN - 1) / BN;
 
@@ -137,42 +136,41 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
             for (int i = 0; i < 16; ++i) oacc[qt][dt][i] = 0.f;
     }
 
-    u32x4 kreg[KPT];
     u32x4 vreg[4];
+    const int krow = (int)(p.ks_s * (int64_t)sizeof(T));  // row pitch in bytes (< 2^25, host-checked)
+    const int vrow = (int)(p.vs_s * (int64_t)sizeof(T));
 
-    auto load_k = [&](int t) {
-#pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-            const int id = i * 256 + tid;
-            const int r = id / DCH, c = id % DCH;
-            const int key = t * BN + r;
-            u32x4 raw = {0u, 0u, 0u, 0u};
-            if (key < p.Sk) raw = ld16(kp + (int64_t)key * p.ks_s + c * 8);
-            kreg[i] = raw;
-        }
+    // Buffer resource over the valid rows of key tile t: offsets past the last row read zeros.
+    auto tile_rsrc = [&](const T* base, int pitch, int64_t stride, int t) {
+        const int rows = min(BN, p.Sk - t * BN);
+        return make_rsrc(base + (int64_t)t * BN * stride, (uint32_t)((rows - 1) * pitch + D * (int)sizeof(T)));
     };
-    auto store_k = [&]() {
+
+    // K tile t -> LDS by direct buffer->LDS loads: one wave instruction fills 1 KB of LDS (lane l ->
+    // byte 16*l), i.e. 1024/(2*D) rows; lane l therefore loads the global chunk that belongs at its
+    // LDS slot, c = slot ^ kswz(row).
+    auto dma_k = [&](T* dst, int t) {
+        constexpr int ROWS_PER_INSTR = 1024 / (2 * D);
+        constexpr int INSTR = BN / ROWS_PER_INSTR / NW;  // per wave
+        const auto rs = tile_rsrc(kp, krow, p.ks_s, t);
 #pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-            const int id = i * 256 + tid;
-            const int r = id / DCH, c = id % DCH;
-            st16(Ks + r * D + 8 * (c ^ kswz<D>(r)), kreg[i]);
+        for (int i = 0; i < INSTR; ++i) {
+            const int r0 = (wave * INSTR + i) * ROWS_PER_INSTR;
+            const int r = r0 + lane / DCH;
+            const int c = (lane % DCH) ^ kswz<D>(r);
+            buf_ld16_lds(rs, dst + r0 * D, (uint32_t)(r * krow + c * 16));
         }
     };
     auto load_v = [&](int t) {
-        if (tid < NVB) {
+        if (NVB == 256 || tid < NVB) {
             const int g = tid / DCH, c = tid % DCH;
+            const auto rs = tile_rsrc(vp, vrow, p.vs_s, t);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = t * BN + 4 * g + i;
-                u32x4 raw = {0u, 0u, 0u, 0u};
-                if (key < p.Sk) raw = ld16(vp + (int64_t)key * p.vs_s + c * 8);
-                vreg[i] = raw;
-            }
+            for (int i = 0; i < 4; ++i) vreg[i] = buf_ld16(rs, (uint32_t)((4 * g + i) * vrow + c * 16));
         }
     };
     auto store_v = [&]() {
-        if (tid < NVB) {
+        if (NVB == 256 || tid < NVB) {
             const int g = tid / DCH, c = tid % DCH;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
@@ -188,24 +186,25 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
         }
     };
 
-    if (nt > 0) {
-        load_k(0);
-        store_k();
-        load_v(0);
-    }
-
-    for (int t = 0; t < nt; ++t) {
-        __syncthreads();
-        if (t + 1 < nt) load_k(t + 1);
+    // One key tile.  Kcur holds K[t]; Knext receives K[t+1] while this tile computes.
+    auto tile = [&](const T* Kcur, T* Knext, int t) {
+        // K[t] (direct-to-LDS) and V[t] (registers) have landed for this wave; after the barrier
+        // every wave's share is visible and every wave has finished tile t-1.
+        wait_vmem();
+        lds_barrier();
+        store_v();
+        if (t + 1 < nt) {
+            load_v(t + 1);
+            dma_k(Knext, t + 1);
+        }
 
         const int kbase = t * BN;
-        const bool wave_skip = CAUSAL && ((int64_t)kbase > (int64_t)wq0 + QT * 32 - 1 + p.delta);
-        const bool need_mask =
-            (kbase + BN > p.Sk) || (CAUSAL && ((int64_t)kbase + BN - 1 > (int64_t)wq0 + p.delta));
+        const bool wave_skip = CAUSAL && (kbase > wq0 + QT * 32 - 1 + p.delta);
+        const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && (kbase + BN - 1 > wq0 + p.delta));
 
-        f32x16 s[QT][KT];
         V8 pb[QT][PVS];
         if (!wave_skip) {
+            f32x16 s[QT][KT];
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
@@ -218,29 +217,24 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
                 for (int kt = 0; kt < KT; ++kt) {
                     const int r = kt * 32 + l32;
                     const int c = ks * 2 + hf;
-                    V8 a = *reinterpret_cast<const V8*>(Ks + r * D + 8 * (c ^ kswz<D>(r)));
+                    V8 a = *reinterpret_cast<const V8*>(Kcur + r * D + 8 * (c ^ kswz<D>(r)));
 #pragma unroll
                     for (int qt = 0; qt < QT; ++qt) s[qt][kt] = Elem<T>::mfma32(a, qf[qt][ks], s[qt][kt]);
                 }
             }
-        }
-
-        store_v();
-
-        if (!wave_skip) {
             if (need_mask) {
+                // Element i of key tile kt holds key kbase + kt*32 + 8*(i/4) + 4*hf + i%4; it is
+                // visible iff its compile-time offset kt*32 + 8*(i/4) + i%4 is <= lim.
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt) {
-                    const int64_t qlim = (int64_t)wq0 + qt * 32 + l32 + p.delta;
+                    int lim = p.Sk - 1 - kbase;
+                    if (CAUSAL) lim = min(lim, wq0 + qt * 32 + l32 + p.delta - kbase);
+                    lim -= 4 * hf;
 #pragma unroll
                     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            const int key = kbase + kt * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
-                            bool vis = key < p.Sk;
-                            if (CAUSAL) vis = vis && ((int64_t)key <= qlim);
-                            if (!vis) s[qt][kt][i] = kNegInf;
-                        }
+                        for (int i = 0; i < 16; ++i)
+                            if (kt * 32 + 8 * (i >> 2) + (i & 3) > lim) s[qt][kt][i] = kNegInf;
                 }
             }
 #pragma unroll
@@ -278,11 +272,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
             }
         }
 
-        __syncthreads();
-        if (t + 1 < nt) {
-            store_k();
-            load_v(t + 1);
-        }
+        lds_barrier();  // V^T of tile t visible
 
         if (!wave_skip) {
 #pragma unroll
@@ -301,11 +291,21 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
                 }
             }
         }
+    };
+
+    if (nt > 0) {
+        dma_k(Ksa, 0);
+        load_v(0);
+    }
+    for (int t = 0; t < nt; t += 2) {  // unrolled by two so each tile names its K buffers statically
+        tile(Ksa, Ksb, t);
+        if (t + 1 < nt) tile(Ksb, Ksa, t + 1);
     }
 
-    // Epilogue: normalise, stage O through LDS for 16-byte coalesced row stores, write LSE.
+    // Epilogue: normalise, stage O through LDS (waves 0-1 in Ksa, 2-3 in Ksb; 16-byte chunk c of
+    // row r at c ^ (r % DCH)) for 16-byte coalesced row stores, and write the LSE.
     __syncthreads();
-    T* Os = reinterpret_cast<T*>(smem) + wave * QT * 32 * OSTR;
+    T* Os = (wave < 2 ? Ksa : Ksb) + (wave & 1) * 32 * D;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         const float l = lrow[qt] + shfl_xor_f(lrow[qt], 32);
@@ -318,7 +318,8 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
                 typename Elem<T>::vec4 o4;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) o4[e] = Elem<T>::from_f32(oacc[qt][dt][4 * i4 + e] * inv);
-                *reinterpret_cast<typename Elem<T>::vec4*>(Os + row * OSTR + dt * 32 + 8 * i4 + 4 * hf) = o4;
+                const int c = dt * 4 + i4;
+                *reinterpret_cast<typename Elem<T>::vec4*>(Os + row * D + 8 * (c ^ (row % DCH)) + 4 * hf) = o4;
             }
         if (p.lse != nullptr && hf == 0) {
             const int qrow = wq0 + row;
@@ -335,7 +336,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
         const int id = it * 64 + lane;
         const int row = id / DCH, c = id % DCH;
         const int qrow = wq0 + row;
-        if (qrow < p.Sq) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Os + row * OSTR + c * 8));
+        if (qrow < p.Sq) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Os + row * D + 8 * (c ^ (row % DCH))));
     }
 }
 
@@ -384,8 +385,9 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     if (a->D != a->Dv)
         return fail(DTATTN_ERR_UNSUPPORTED, "prefill: D=%lld != Dv=%lld not supported", (long long)a->D,
                     (long long)a->Dv);
-    if (a->Sq > 0x3fffffff || a->Sk > 0x3fffffff || a->B * a->Hq > 0x3fffffff)
-        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: sizes exceed 2^30");
+    // Sequence lengths up to 2^29 keep every causal index expression of the kernels in int32.
+    if (a->Sq > (1 << 29) || a->Sk > (1 << 29) || a->B * a->Hq > 0x3fffffff)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: sequence length exceeds 2^29");
     if (a->B == 0 || a->Sq == 0) return DTATTN_OK;
     if (a->q == nullptr || a->o == nullptr || (a->Sk > 0 && (a->k == nullptr || a->v == nullptr)))
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill: null tensor pointer");
@@ -401,6 +403,9 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     }
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
         return fail(DTATTN_ERR_UNSUPPORTED, "prefill: tensors must be 16-byte aligned");
+    // key/value tiles are addressed with 32-bit byte offsets: 64 rows x row pitch < 2^31
+    if (a->k_stride[2] * esz_in * 64 >= (int64_t)1 << 31 || a->v_stride[2] * esz_in * 64 >= (int64_t)1 << 31)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: key/value row pitch exceeds 32 MB");
     const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
     const float c = scale * kLog2e;
     int64_t delta64 = a->q_offset - a->k_offset;

@@ -135,8 +135,9 @@ def test_deterministic():
 def _sampled_check(o, lse, q, k, v, pairs, causal, q_offset=0, k_offset=0):
     for b, h in pairs:
         hk = h // (q.shape[1] // k.shape[1])
-        ro, rl = orc.sdpa_fwd(rounded(q[b, h]), rounded(k[b, hk]), rounded(v[b, hk]), is_causal=causal,
-                              q_offset=q_offset, k_offset=k_offset)
+        ro, rl = orc.sdpa_fwd(rounded(q[b, h])[None], rounded(k[b, hk])[None], rounded(v[b, hk])[None],
+                              is_causal=causal, q_offset=q_offset, k_offset=k_offset)
+        ro, rl = ro[0], rl[0]
         assert max_abs(host(o[b, h]), ro) <= O_TOL_BF16, (b, h)
         assert lse_rel(host(lse[b, h]), rl) <= LSE_TOL, (b, h)
 
