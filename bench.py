@@ -68,6 +68,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extras", action="store_true", help="only the headline prefill")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 3 device copies of 1 GiB (known traffic) to scale rocprof byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the attention "
@@ -83,6 +85,14 @@ def main():
         f"PFLOP/s, fp8 {pk.fp8_flops / 1e15:.2f} PFLOP/s (computed); published peaks used: bf16 2.5, fp8 5.0 "
         f"PFLOP/s, HBM 8.0 TB/s")
     timer = Timer(torch)
+    if args.copy_calibration:
+        src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log("copy calibration: 3 x copy of 1 GiB (1,048,576 KiB read and written per launch)")
 
     # ---------------------------------------------------------------- headline: Llama prefill
     B, Hq, Hkv, S, D = 4, 32, 8, 2048, 128

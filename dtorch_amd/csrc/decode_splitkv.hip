@@ -132,8 +132,7 @@ __global__ void __launch_bounds__(256) decode_partial_kernel(const DecodeParams 
             float mx = kNegInf;
 #pragma unroll
             for (int i = 0; i < NI; ++i) mx = fmaxf(mx, sc[i][g]);
-#pragma unroll
-            for (int mk = LPT; mk < 64; mk <<= 1) mx = fmaxf(mx, shfl_xor_f(mx, mk));
+            mx = max_across_groups<LPT>(mx);
             const float mnew = fmaxf(m[g], mx);
             const float mbase = mnew == kNegInf ? 0.f : mnew;
             const float alpha = fast_exp2(m[g] - mbase);
@@ -162,15 +161,9 @@ __global__ void __launch_bounds__(256) decode_partial_kernel(const DecodeParams 
     // reduce across the TPI token lanes of each row position (same c8), then across waves
 #pragma unroll
     for (int g = 0; g < G; ++g) {
+        l[g] = sum_across_groups<LPT>(l[g]);
 #pragma unroll
-        for (int mk = LPT; mk < 64; mk <<= 1) l[g] += shfl_xor_f(l[g], mk);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float x = acc[g][e];
-#pragma unroll
-            for (int mk = LPT; mk < 64; mk <<= 1) x += shfl_xor_f(x, mk);
-            acc[g][e] = x;
-        }
+        for (int e = 0; e < 8; ++e) acc[g][e] = sum_across_groups<LPT>(acc[g][e]);
     }
     if (tsub == 0) {
 #pragma unroll

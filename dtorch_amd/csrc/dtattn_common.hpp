@@ -138,6 +138,54 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// Cross-row exchanges on gfx950 (VALU, no LDS round trip).  v_permlane32_swap with both operands
+// equal to x returns {x[l], x[l^32]} in some order in every lane, and v_permlane16_swap returns
+// {x[l], x[l^16]}; combining the pair with a commutative op is the xor-32 / xor-16 butterfly step.
+__device__ __forceinline__ void pair32(float x, float& a, float& b) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    a = __builtin_bit_cast(float, (unsigned)r[0]);
+    b = __builtin_bit_cast(float, (unsigned)r[1]);
+}
+__device__ __forceinline__ void pair16(float x, float& a, float& b) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    a = __builtin_bit_cast(float, (unsigned)r[0]);
+    b = __builtin_bit_cast(float, (unsigned)r[1]);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    float a, b;
+    pair32(x, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    float a, b;
+    pair32(x, a, b);
+    return a + b;
+}
+__device__ __forceinline__ float max_xor16(float x) {
+    float a, b;
+    pair16(x, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    float a, b;
+    pair16(x, a, b);
+    return a + b;
+}
+
+// Reductions over the lanes that share lane % N (N = 8 or 16), i.e. across the 64/N lane groups.
+template <int N>
+__device__ __forceinline__ float sum_across_groups(float x) {
+    if (N == 8) x += dpp_f<0x128>(x);  // row_ror:8 == lane ^ 8 within a row of 16
+    return sum_xor32(sum_xor16(x));
+}
+template <int N>
+__device__ __forceinline__ float max_across_groups(float x) {
+    if (N == 8) x = fmaxf(x, dpp_f<0x128>(x));
+    return max_xor32(max_xor16(x));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Workgroup barrier for LDS producer/consumer hand-offs: waits only for this wave's LDS operations

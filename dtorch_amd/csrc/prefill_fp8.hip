@@ -238,7 +238,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
             for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
-            mx = fmaxf(mx, shfl_xor_f(mx, 32));
+            mx = max_xor32(mx);
             const float mnew = fmaxf(mrow, mx * cq);
             const float mbase = (mnew == kNegInf) ? 0.f : mnew;
             const float alpha = fast_exp2(mrow - mbase);
@@ -289,7 +289,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
     __syncthreads();
     bf16_t* Os = reinterpret_cast<bf16_t*>(smem) + wave * 32 * OSTR;
     {
-        const float l = lrow + shfl_xor_f(lrow, 32);
+        const float l = sum_xor32(lrow);
         const float inv = l > 0.f ? vdesc / l : 0.f;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)

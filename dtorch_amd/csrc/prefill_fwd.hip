@@ -47,7 +47,45 @@ struct PrefillParams {
     int32_t n_qblocks;
     int32_t delta;  // key j visible to query i iff j <= i + delta (causal only)
     float c;        // softmax scale * log2(e)
+    int32_t xcd_map;  // 1: group the workgroups of each (batch, kv head) slice on one XCD
 };
+
+// Workgroup -> (query block, batch, query head).  Causal launches take the longest query blocks
+// first.  Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8), each with its own L2;
+// with xcd_map the slices (b, kv head) are dealt to XCDs so that every workgroup reading a slice's
+// K/V runs on the same XCD and the slice is fetched from HBM once per L2 instead of once per XCD.
+struct BlockCoord {
+    int qb, b, hq, hk;
+};
+
+template <bool CAUSAL>
+__device__ __forceinline__ BlockCoord block_coord(const PrefillParams& p) {
+    const int bid = blockIdx.x;
+    BlockCoord r;
+    if (p.xcd_map) {
+        const int x = bid & 7, j = bid >> 3;
+        const int per_rank = (p.B * p.Hkv / 8) * p.group;  // workgroups per query-block rank per XCD
+        const int rank = j / per_rank, rem = j % per_rank;
+        const int slice = (rem / p.group) * 8 + x;
+        r.b = slice / p.Hkv;
+        r.hk = slice % p.Hkv;
+        r.hq = r.hk * p.group + rem % p.group;
+        r.qb = CAUSAL ? (p.n_qblocks - 1 - rank) : rank;
+    } else {
+        const int bh = p.B * p.Hq;
+        const int rest = bid % bh;
+        r.qb = CAUSAL ? (p.n_qblocks - 1 - bid / bh) : (bid / bh);
+        r.hq = rest % p.Hq;
+        r.b = rest / p.Hq;
+        r.hk = r.hq / p.group;
+    }
+    return r;
+}
+
+// Lazy rescaling: the running max only moves (and O, l are only rescaled) when some row's max grew
+// by more than 2^8; otherwise P is taken against the stale max (values up to 2^8, exact in the
+// normalisation, which uses the same max for O and l).
+constexpr float kRescaleThreshold = 8.0f;
 
 template <int D>
 __device__ __forceinline__ int kswz(int r) {
@@ -89,13 +127,8 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     const int l32 = lane & 31;
     const int hf = lane >> 5;
 
-    const int bh = p.B * p.Hq;
-    const int bid = blockIdx.x;
-    const int qb = CAUSAL ? (p.n_qblocks - 1 - bid / bh) : (bid / bh);
-    const int rest = bid % bh;
-    const int hq = rest % p.Hq;
-    const int b = rest / p.Hq;
-    const int hk = hq / p.group;
+    const BlockCoord bc = block_coord<CAUSAL>(p);
+    const int qb = bc.qb, b = bc.b, hq = bc.hq, hk = bc.hk;
 
     const T* qp = reinterpret_cast<const T*>(p.q) + b * p.qs_b + hq * p.qs_h;
     const T* kp = reinterpret_cast<const T*>(p.k) + b * p.ks_b + hk * p.ks_h;
@@ -244,16 +277,19 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
                 for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
                     for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[qt][kt][i]);
-                mx = fmaxf(mx, shfl_xor_f(mx, 32));
-                const float mnew = fmaxf(mrow[qt], mx * p.c);
-                const float mbase = (mnew == kNegInf) ? 0.f : mnew;
-                const float alpha = fast_exp2(mrow[qt] - mbase);
-                mrow[qt] = mnew;
-                float ls = lrow[qt] * alpha;
+                mx = max_xor32(mx);
+                const float mcand = fmaxf(mrow[qt], mx * p.c);
+                if (__any(mcand - mrow[qt] > kRescaleThreshold)) {  // wave-uniform
+                    const float alpha = fast_exp2(mrow[qt] - (mcand == kNegInf ? 0.f : mcand));
+                    mrow[qt] = mcand;
+                    lrow[qt] *= alpha;
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt)
+                    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) oacc[qt][dt][i] *= alpha;
+                        for (int i = 0; i < 16; ++i) oacc[qt][dt][i] *= alpha;
+                }
+                const float mbase = (mrow[qt] == kNegInf) ? 0.f : mrow[qt];
+                float ls = lrow[qt];
 #pragma unroll
                 for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
@@ -308,7 +344,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     T* Os = (wave < 2 ? Ksa : Ksb) + (wave & 1) * 32 * D;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        const float l = lrow[qt] + shfl_xor_f(lrow[qt], 32);
+        const float l = sum_xor32(lrow[qt]);
         const float inv = l > 0.f ? 1.f / l : 0.f;
         const int row = qt * 32 + l32;
 #pragma unroll
@@ -445,6 +481,7 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     p.n_qblocks = 0;
     p.delta = delta;
     p.c = c;
+    p.xcd_map = (p.B * p.Hkv) % 8 == 0 ? 1 : 0;
     const int D = (int)a->D;
     const bool causal = a->causal != 0;
     if (a->dtype == DTATTN_BF16) return dispatch_prefill<bf16_t>(p, D, causal, stream);
