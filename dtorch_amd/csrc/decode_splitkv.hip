@@ -5,15 +5,16 @@
 // (dtorch/core/operators/standard/scaled_dot_product_attention_op.cc:107-109) at Lq = 1,
 // is_causal = False, over the true length.  The reference has no KV cache or decode op.
 //
-// Kernel 1 (decode_partial_kernel): one workgroup per (b, kv head, chunk of C tokens, head subgroup).
-//   The G query heads of the subgroup share every K/V byte read.  A token row (D * 2 bytes) is read
-//   by D/8 lanes with 16-byte loads, so each load instruction covers whole rows (fully coalesced).
-//   Scores use v_dot2_f32_{bf16,f16} and a butterfly over the D/8 lanes of the row; the chunk's
-//   softmax runs in LDS; P V accumulates in fp32 registers and is reduced across lanes and waves.
-//   Output: a partial O (normalised by its own sum) and a partial LSE per (b, head, chunk).
-//   Chunks past L_b exit immediately; rows at or past L_b are never read.
+// Kernel 1 (decode_kernel): a workgroup owns (b, kv head, chunk of C tokens, head subgroup of G query
+// heads); the G heads share every K/V byte read.  A token row (D * 2 bytes) is read by D/8 lanes with
+// 16-byte buffer loads (whole rows per load instruction; rows past L_b read zeros without touching
+// memory).  Scores: v_dot2_f32 chain + a DPP row sum; online softmax per wave; P V with v_dot2 over
+// token pairs (P rounded to the element type, as the prefill's PV MFMA does); the 4 waves combine
+// through LDS and write a partial (O, LSE) per chunk -- or the final output when the sequence is a
+// single chunk.
 // Kernel 2 (decode_merge_kernel): one wave per (b, query head) merges the ceil(L_b / C) partials by
-//   LSE and writes O in the input dtype plus the fp32 LSE.
+// LSE.  (Merging inside kernel 1 by the last workgroup needs device-scope fences; on gfx950 each one
+// writes back and invalidates the XCD's L2, which costs far more than the second launch.)
 #include "dtattn_common.hpp"
 
 namespace dtattn {
@@ -37,7 +38,7 @@ struct DecodeParams {
     float c;  // scale * log2(e)
 };
 
-constexpr int kDecodeChunk = 256;
+constexpr int kDecodeChunk = 128;
 
 size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk, int64_t* nsplit_out) {
     const int64_t nsplit = (S_max + chunk - 1) / chunk;
@@ -47,22 +48,17 @@ size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t 
     return ((o_bytes + 255) & ~(size_t)255) + ((lse_bytes + 255) & ~(size_t)255);
 }
 
-// G heads per workgroup, D head dim, TPW tokens per wave (chunk = 4 * TPW).  A wave walks its
-// tokens in sub-blocks of SB = min(TPW, 64) tokens; all loops have compile-time trip counts, so the
-// K and V loads of a sub-block are issued together (and the compiler may hoist the next sub-block's).
-// Loads go through a buffer resource over the chunk's valid rows: rows past the sequence read zeros
-// without a branch.  A token row is read by D/8 lanes (one DPP row for D = 128), so the score is a
-// v_dot2 chain plus a DPP row sum; the chunk softmax is online per wave, and the 4 waves combine once
-// through LDS.
+// G heads per workgroup, D head dim, TPW tokens per wave (chunk = 4 * TPW, sub-blocks of at most 64
+// tokens per wave; all trip counts are compile-time so each sub-block's loads issue together).
 template <typename T, int D, int G, int TPW>
-__global__ void __launch_bounds__(256) decode_partial_kernel(const DecodeParams p) {
+__global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     constexpr int LPT = D / 8;            // lanes per token row
     constexpr int TPI = 64 / LPT;         // tokens per wave-wide load
     constexpr int SB = TPW < 64 ? TPW : 64;
     constexpr int NSB = TPW / SB;         // sub-blocks per wave
     constexpr int NI = SB / TPI;          // K (and V) loads per lane per sub-block
     constexpr int C = 4 * TPW;
-    static_assert(NI >= 1 && TPW % SB == 0, "bad chunk");
+    static_assert(NI >= 2 && NI % 2 == 0 && TPW % SB == 0, "bad chunk");
     __shared__ float red_o[4][G][D];
     __shared__ float red_m[4][G];
     __shared__ float red_l[4][G];
@@ -75,10 +71,20 @@ __global__ void __launch_bounds__(256) decode_partial_kernel(const DecodeParams 
     const int sg = blockIdx.y / p.Hkv;   // head subgroup within the kv group
     const int b = blockIdx.z;
     const int L = min(max(p.lengths[b], 0), p.S_max);  // never read past the cache
+    const int ns = (L + C - 1) / C;      // chunks of this sequence
     const int t0 = split * C;
+    const int hq0 = hk * p.group + sg * G;
+    T* obase = reinterpret_cast<T*>(p.o) + b * p.os_b;
+    if (L == 0) {  // empty sequence: O = 0, LSE = -inf
+        if (split == 0)
+            for (int idx = tid; idx < G * D; idx += 256) {
+                obase[(hq0 + idx / D) * p.os_h + idx % D] = Elem<T>::from_f32(0.f);
+                if (p.lse != nullptr && idx % D == 0) p.lse[b * p.lses_b + hq0 + idx / D] = kNegInf;
+            }
+        return;
+    }
     if (t0 >= L) return;
     const int n_tok = min(C, L - t0);
-    const int hq0 = hk * p.group + sg * G;
     const int c8 = lane % LPT;           // 16-byte chunk of the row this lane reads
     const int tsub = lane / LPT;
 
@@ -148,14 +154,22 @@ __global__ void __launch_bounds__(256) decode_partial_kernel(const DecodeParams 
             }
             l[g] = ls;
         }
+        // P V over token pairs (loads i, i+1 hold tokens t, t+TPI of the same row chunk): pack
+        // (v_t[e], v_t'[e]) and (p_t, p_t') as element pairs and accumulate with v_dot2.
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            float vf[8];
-            unpack8<T>(vr[i], vf);
+        for (int i = 0; i < NI; i += 2) {
+            uint32_t vp2[8];
 #pragma unroll
-            for (int g = 0; g < G; ++g)
+            for (int w = 0; w < 4; ++w) {
+                vp2[2 * w] = pack_lo_hi(vr[i][w], vr[i + 1][w], 0);
+                vp2[2 * w + 1] = pack_lo_hi(vr[i][w], vr[i + 1][w], 1);
+            }
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] = __builtin_fmaf(sc[i][g], vf[e], acc[g][e]);
+            for (int g = 0; g < G; ++g) {
+                const uint32_t pp = pack2<T>(sc[i][g], sc[i + 1][g]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] = Elem<T>::dot2(vp2[e], pp, acc[g][e]);
+            }
         }
     }
     // reduce across the TPI token lanes of each row position (same c8), then across waves
@@ -179,6 +193,7 @@ __global__ void __launch_bounds__(256) decode_partial_kernel(const DecodeParams 
         }
     }
     __syncthreads();
+    const bool single = ns == 1;  // the whole sequence is this chunk: write the final output
     for (int idx = tid; idx < G * D; idx += 256) {
         const int g = idx / D, d = idx % D;
         float M = kNegInf;
@@ -192,12 +207,18 @@ __global__ void __launch_bounds__(256) decode_partial_kernel(const DecodeParams 
             val += f * red_o[w][g][d];
         }
         const int hq = hq0 + g;
-        p.part_o[(((int64_t)b * p.Hq + hq) * p.nsplit + split) * D + d] = val / Lsum;
-        if (d == 0) p.part_lse[((int64_t)b * p.Hq + hq) * p.nsplit + split] = (M + __log2f(Lsum)) * kLn2;
+        if (single) {  // the whole sequence was this chunk: final output
+            obase[hq * p.os_h + d] = Elem<T>::from_f32(val / Lsum);
+            if (p.lse != nullptr && d == 0) p.lse[b * p.lses_b + hq] = (M + __log2f(Lsum)) * kLn2;
+        } else {
+            p.part_o[(((int64_t)b * p.Hq + hq) * p.nsplit + split) * D + d] = val / Lsum;
+            if (d == 0) p.part_lse[((int64_t)b * p.Hq + hq) * p.nsplit + split] = (M + __log2f(Lsum)) * kLn2;
+        }
     }
 }
 
-// One wave per (b, query head).
+// One wave per (b, query head): merge the ceil(L_b / C) partials by LSE (sequences that fit in one
+// chunk were written directly by decode_kernel).
 template <typename T, int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p) {
     constexpr int DPL = D / 64;  // d values per lane
@@ -207,16 +228,9 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p)
     const int b = (int)(pair / p.Hq), hq = (int)(pair % p.Hq);
     const int L = min(max(p.lengths[b], 0), p.S_max);
     const int ns = (L + p.chunk - 1) / p.chunk;
-    T* op = reinterpret_cast<T*>(p.o) + b * p.os_b + hq * p.os_h;
-    if (ns == 0) {  // empty sequence: O = 0, LSE = -inf
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) op[lane * DPL + e] = Elem<T>::from_f32(0.f);
-        if (p.lse != nullptr && lane == 0) p.lse[b * p.lses_b + hq] = kNegInf;
-        return;
-    }
+    if (ns <= 1) return;
     const float* pl = p.part_lse + pair * p.nsplit;
     const float* po = p.part_o + pair * p.nsplit * D;
-
     float mx = kNegInf;
     for (int s = lane; s < ns; s += 64) mx = fmaxf(mx, pl[s]);
     mx = wave_max(mx);
@@ -231,6 +245,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p)
 #pragma unroll
         for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(w, po[(int64_t)s * D + lane * DPL + e], acc[e]);
     }
+    T* op = reinterpret_cast<T*>(p.o) + b * p.os_b + hq * p.os_h;
 #pragma unroll
     for (int e = 0; e < DPL; ++e) op[lane * DPL + e] = Elem<T>::from_f32(acc[e]);
     if (p.lse != nullptr && lane == 0) p.lse[b * p.lses_b + hq] = mx + __logf(sum);
@@ -238,9 +253,9 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p)
 
 template <typename T, int D, int G, int TPW>
 static int launch_decode(const DecodeParams& p, hipStream_t stream) {
-    dim3 grid1((unsigned)p.nsplit, (unsigned)(p.Hkv * (p.group / G)), (unsigned)p.B);
-    hipLaunchKernelGGL((decode_partial_kernel<T, D, G, TPW>), grid1, dim3(256), 0, stream, p);
-    int st = check_launch("decode_partial_kernel");
+    dim3 grid((unsigned)p.nsplit, (unsigned)(p.Hkv * (p.group / G)), (unsigned)p.B);
+    hipLaunchKernelGGL((decode_kernel<T, D, G, TPW>), grid, dim3(256), 0, stream, p);
+    int st = check_launch("decode_kernel");
     if (st != DTATTN_OK) return st;
     const int64_t pairs = (int64_t)p.B * p.Hq;
     hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, stream, p);

@@ -80,6 +80,21 @@ __device__ __forceinline__ u32x4 pack8(const float* in) {
     return __builtin_bit_cast(u32x4, v);
 }
 
+// (low or high 16-bit half e of a) | (same half of b) << 16
+__device__ __forceinline__ uint32_t pack_lo_hi(uint32_t a, uint32_t b, int e) {
+    return __builtin_amdgcn_perm(b, a, e ? 0x07060302u : 0x05040100u);
+}
+
+// Two floats rounded to the element type and packed as an element pair.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+    typedef T pair __attribute__((ext_vector_type(2)));
+    pair v;
+    v[0] = Elem<T>::from_f32(x);
+    v[1] = Elem<T>::from_f32(y);
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // ---- raw memory access ------------------------------------------------------------------------
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }

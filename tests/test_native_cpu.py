@@ -107,12 +107,13 @@ def test_empty_problem_is_a_no_op():
 def test_workspace_sizes():
     lib.dtattn_decode_workspace_size.restype = ctypes.c_size_t
     lib.dtattn_decode_workspace_size.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_int32]
-    n = lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 256)
-    nsplit = 8192 // 256
+    n = lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 128)
+    nsplit = 8192 // 128
     o_bytes = 64 * 32 * nsplit * 128 * 4
     lse_bytes = 64 * 32 * nsplit * 4
-    assert n == o_bytes + ((lse_bytes + 255) // 256) * 256
-    assert lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 0) == n  # default chunk 256
+    up = lambda x: (x + 255) // 256 * 256
+    assert n == up(o_bytes) + up(lse_bytes)
+    assert lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 0) == n  # default chunk 128
     lib.dtattn_fp8_quantize_workspace_size.restype = ctypes.c_size_t
     lib.dtattn_fp8_quantize_workspace_size.argtypes = [ctypes.c_int64] * 4
     assert lib.dtattn_fp8_quantize_workspace_size(1, 24, 4608, 128) == ((24 * 18 * 4 + 255) // 256) * 256
