@@ -116,6 +116,19 @@ __device__ __forceinline__ void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
 }
 
+// Same load issued from inline assembly, so the compiler's wait-count pass does not track it (it
+// cannot always prove that later reads of other LDS buffers do not alias the copy and would drain it
+// with vmcnt(0)).  The caller owns completion: an explicit wait_vmem() plus a barrier before any wave
+// reads the destination.
+__device__ __forceinline__ void buf_ld16_lds_async(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
+    // a flat pointer into LDS carries the LDS byte offset in its low 32 bits
+    const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_addr), "v"(voffset), "s"(r)
+                 : "m0");
+}
+
 // ---- wave helpers -----------------------------------------------------------------------------
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }

@@ -11,20 +11,19 @@
 // Layout trick
 //   The score tile is computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_{bf16,f16}: the
 //   accumulator column (lane % 32) is the query, so each lane holds 16 keys of one query row and the
-//   row max / row sum need one cross-half exchange (lane ^ 32) instead of a 32-lane reduction.  The
+//   row max needs one cross-half exchange (v_permlane32_swap) instead of a 32-lane reduction.  The
 //   output is accumulated transposed as well, O^T = V^T P^T: P^T comes straight from the score
-//   registers (the MFMA reduction index is a free permutation, matched on both operands), and V is
-//   written transposed into LDS so each lane reads 4 consecutive keys of one d with one 8-byte read.
-//   The per-query rescale factor is then a per-lane scalar.
+//   registers (the MFMA reduction index is a free permutation, matched on both operands), and the V^T
+//   operand is read from the row-major V tile with ds_read_b64_tr_b16 (LDS transpose read).  The
+//   per-query rescale factor is then a per-lane scalar.
 //
-// LDS layouts (bank-conflict free for the 16-byte K reads and the 8-byte V^T reads/writes)
-//   K  tile: [64 keys][D], 16-byte chunk c of row r stored at chunk c ^ kswz(r).
-//   V^T tile: [D][64 keys], 4-key group g of row d stored at group g ^ ((d & 15) ^ ((d >> 4) & 15)).
+// LDS: K and V tiles of 64 rows, double-buffered, filled by direct buffer->LDS loads (no VGPR
+// staging); 16-byte chunk c of row r sits at chunk c ^ kswz(r), which keeps the 16-byte K reads and
+// the 8-byte transposed V reads spread over the banks.
 //
-// Pipeline per key tile j (K double-buffered in LDS and filled by direct global->LDS loads, V
-// prefetched one tile ahead in registers and transposed into a single V^T buffer):
-//   wait + barrier | V[j] regs -> V^T | V[j+1] -> regs (async) | K[j+1] -> LDS (async) |
-//   S = K[j] Q^T | softmax | barrier | O^T += V^T P^T
+// Pipeline per key tile j (one barrier per tile):
+//   wait own loads + barrier | K[j+1], V[j+1] -> LDS (async) | S^T = K[j] Q^T | softmax |
+//   O^T += V^T(j) P^T(j)
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -92,34 +91,29 @@ __device__ __forceinline__ int kswz(int r) {
     return D >= 128 ? (r & 15) : (r & 7);
 }
 
-__device__ __forceinline__ int vswz(int d) { return (d & 15) ^ ((d >> 4) & 15); }
-
-// Pack the (e)-th 16-bit half of two dwords into one dword: low half from a, high half from b.
-__device__ __forceinline__ uint32_t pack_half(uint32_t a, uint32_t b, int e) {
-    return __builtin_amdgcn_perm(b, a, e ? 0x07060302u : 0x05040100u);
-}
-
 template <typename T, int D, int QT, bool CAUSAL>
 __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams p) {
     constexpr int NW = 4;
     constexpr int BN = 64;
-    constexpr int BM = NW * QT * 32;
+    constexpr int BM = NW * 32;
     constexpr int DCH = D / 8;            // 16-byte chunks per row
-    constexpr int KSTEPS = D / 16;        // MFMA k-steps of S = K Q^T
+    constexpr int KSTEPS = D / 16;        // MFMA k-steps of S^T = K Q^T
     constexpr int DT = D / 32;            // 32-row d tiles of O^T
     constexpr int KT = BN / 32;           // 32-key tiles per key block
     constexpr int PVS = BN / 16;          // MFMA k-steps of O^T = V^T P^T
-    constexpr int NVB = (BN / 4) * DCH;   // 4-key x 8-d blocks of V per tile
-    static_assert((BN * DCH) % 256 == 0, "tile/thread mismatch");
-    static_assert(NVB <= 256, "one V block per thread at most");
-    static_assert(QT == 1, "the output staging reuses the two K buffers: 2 waves x 32 rows each");
+    static_assert(QT == 1, "one 32-query tile per wave");
     typedef typename Elem<T>::vec8 V8;
+    typedef typename Elem<T>::vec4 V4;
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-    // Three distinct LDS objects so the compiler's alias analysis can tell the in-flight K load
-    // (into one buffer) from the reads of the other buffer and from the V^T writes.
-    __shared__ __attribute__((aligned(16))) T Ksa[BN * D];
-    __shared__ __attribute__((aligned(16))) T Ksb[BN * D];
-    __shared__ __attribute__((aligned(16))) T VTs[D * BN];
+    // K and V tiles, double-buffered, each [64 keys][D] with 16-byte chunk c of row r at c ^ kswz(r).
+    // Four distinct LDS objects so the compiler's alias analysis can tell an in-flight load into one
+    // buffer from the reads of the others.
+    __shared__ __attribute__((aligned(16))) T Ka[BN * D];
+    __shared__ __attribute__((aligned(16))) T Kb[BN * D];
+    __shared__ __attribute__((aligned(16))) T Va[BN * D];
+    __shared__ __attribute__((aligned(16))) T Vb[BN * D];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -135,7 +129,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     const T* vp = reinterpret_cast<const T*>(p.v) + b * p.vs_b + hk * p.vs_h;
 
     const int q0 = qb * BM;
-    const int wq0 = q0 + wave * QT * 32;
+    const int wq0 = q0 + wave * 32;
 
     int kend = p.Sk;
     if (CAUSAL) {
@@ -145,222 +139,181 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     const int nt = (kend + BN - 1) / BN;
 
     // Q fragments (B operand of S^T = K Q^T): lane holds query l32, d = ks*16 + hf*8 .. +8.
-    V8 qf[QT][KSTEPS];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        const int qrow = wq0 + qt * 32 + l32;
+    V8 qf[KSTEPS];
+    {
+        const int qrow = wq0 + l32;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             u32x4 raw = {0u, 0u, 0u, 0u};
             if (qrow < p.Sq) raw = ld16(qp + (int64_t)qrow * p.qs_s + ks * 16 + hf * 8);
-            qf[qt][ks] = __builtin_bit_cast(V8, raw);
+            qf[ks] = __builtin_bit_cast(V8, raw);
         }
     }
 
-    f32x16 oacc[QT][DT];
-    float mrow[QT], lrow[QT];
+    f32x16 oacc[DT];
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        mrow[qt] = kNegInf;
-        lrow[qt] = 0.f;
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) oacc[qt][dt][i] = 0.f;
-    }
+        for (int i = 0; i < 16; ++i) oacc[dt][i] = 0.f;
+    float mrow = kNegInf, lrow = 0.f;
 
-    u32x4 vreg[4];
     const int krow = (int)(p.ks_s * (int64_t)sizeof(T));  // row pitch in bytes (< 2^25, host-checked)
     const int vrow = (int)(p.vs_s * (int64_t)sizeof(T));
 
-    // Buffer resource over the valid rows of key tile t: offsets past the last row read zeros.
-    auto tile_rsrc = [&](const T* base, int pitch, int64_t stride, int t) {
-        const int rows = min(BN, p.Sk - t * BN);
-        return make_rsrc(base + (int64_t)t * BN * stride, (uint32_t)((rows - 1) * pitch + D * (int)sizeof(T)));
-    };
-
-    // K tile t -> LDS by direct buffer->LDS loads: one wave instruction fills 1 KB of LDS (lane l ->
-    // byte 16*l), i.e. 1024/(2*D) rows; lane l therefore loads the global chunk that belongs at its
-    // LDS slot, c = slot ^ kswz(row).
-    auto dma_k = [&](T* dst, int t) {
+    // Tile t of K or V -> LDS by direct buffer->LDS loads: one wave instruction fills 1 KB of LDS (lane
+    // l -> byte 16*l), i.e. 1024/(2*D) rows, so lane l loads the global chunk that belongs at its LDS
+    // slot, c = slot ^ kswz(row).  The buffer resource covers the tile's valid rows; rows past Sk
+    // read zeros.
+    auto dma = [&](T* dst, const T* base, int pitch, int64_t stride, int t) {
         constexpr int ROWS_PER_INSTR = 1024 / (2 * D);
         constexpr int INSTR = BN / ROWS_PER_INSTR / NW;  // per wave
-        const auto rs = tile_rsrc(kp, krow, p.ks_s, t);
+        const int rows = min(BN, p.Sk - t * BN);
+        const auto rs = make_rsrc(base + (int64_t)t * BN * stride,
+                                  (uint32_t)((rows - 1) * pitch + D * (int)sizeof(T)));
 #pragma unroll
         for (int i = 0; i < INSTR; ++i) {
             const int r0 = (wave * INSTR + i) * ROWS_PER_INSTR;
             const int r = r0 + lane / DCH;
             const int c = (lane % DCH) ^ kswz<D>(r);
-            buf_ld16_lds(rs, dst + r0 * D, (uint32_t)(r * krow + c * 16));
-        }
-    };
-    auto load_v = [&](int t) {
-        if (NVB == 256 || tid < NVB) {
-            const int g = tid / DCH, c = tid % DCH;
-            const auto rs = tile_rsrc(vp, vrow, p.vs_s, t);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) vreg[i] = buf_ld16(rs, (uint32_t)((4 * g + i) * vrow + c * 16));
-        }
-    };
-    auto store_v = [&]() {
-        if (NVB == 256 || tid < NVB) {
-            const int g = tid / DCH, c = tid % DCH;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int d = c * 8 + 2 * w + e;
-                    u32x2 pr;
-                    pr.x = pack_half(vreg[0][w], vreg[1][w], e);
-                    pr.y = pack_half(vreg[2][w], vreg[3][w], e);
-                    *reinterpret_cast<u32x2*>(VTs + d * BN + 4 * (g ^ vswz(d))) = pr;
-                }
-            }
+            buf_ld16_lds_async(rs, dst + r0 * D, (uint32_t)(r * pitch + c * 16));
         }
     };
 
-    // One key tile.  Kcur holds K[t]; Knext receives K[t+1] while this tile computes.
-    auto tile = [&](const T* Kcur, T* Knext, int t) {
-        // K[t] (direct-to-LDS) and V[t] (registers) have landed for this wave; after the barrier
-        // every wave's share is visible and every wave has finished tile t-1.
+    // V^T fragments for the PV MFMA come straight from the row-major V tile with ds_read_b64_tr_b16:
+    // within each 16-lane block, lane 4j+a addresses key K0+j, d-segment D0+4a, and lane i then
+    // receives V[K0..K0+3][D0+i] -- one d and four consecutive keys, the A-operand slot layout.
+    const int blk = lane >> 4, bl = lane & 15;
+    const int tr_key = bl >> 2;                 // j
+    const int tr_d = 16 * (blk & 1) + 4 * (bl & 3);  // D0 offset within the 32-d tile + 4a
+    const int tr_k4 = 4 * (blk >> 1);           // 4 * hf
+
+    // One key tile.  Kc/Vc hold tile t; Kn/Vn receive tile t+1.
+    auto tile = [&](const T* Kc, const T* Vc, T* Kn, T* Vn, int t) {
         wait_vmem();
-        lds_barrier();
-        store_v();
+        lds_barrier();  // tile t landed everywhere; every wave finished tile t-1 (so Kn/Vn are free)
         if (t + 1 < nt) {
-            load_v(t + 1);
-            dma_k(Knext, t + 1);
+            dma(Kn, kp, krow, p.ks_s, t + 1);
+            dma(Vn, vp, vrow, p.vs_s, t + 1);
         }
-
         const int kbase = t * BN;
-        const bool wave_skip = CAUSAL && (kbase > wq0 + QT * 32 - 1 + p.delta);
+        if (CAUSAL && kbase > wq0 + 31 + p.delta) return;  // every row of this wave precedes the tile
         const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && (kbase + BN - 1 > wq0 + p.delta));
 
-        V8 pb[QT][PVS];
-        if (!wave_skip) {
-            f32x16 s[QT][KT];
+        f32x16 s[KT];
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt)
+        for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-                for (int kt = 0; kt < KT; ++kt)
+            for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) s[qt][kt][i] = 0.f;
+        for (int ks = 0; ks < KSTEPS; ++ks) {
 #pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) {
-#pragma unroll
-                for (int kt = 0; kt < KT; ++kt) {
-                    const int r = kt * 32 + l32;
-                    const int c = ks * 2 + hf;
-                    V8 a = *reinterpret_cast<const V8*>(Kcur + r * D + 8 * (c ^ kswz<D>(r)));
-#pragma unroll
-                    for (int qt = 0; qt < QT; ++qt) s[qt][kt] = Elem<T>::mfma32(a, qf[qt][ks], s[qt][kt]);
-                }
-            }
-            if (need_mask) {
-                // Element i of key tile kt holds key kbase + kt*32 + 8*(i/4) + 4*hf + i%4; it is
-                // visible iff its compile-time offset kt*32 + 8*(i/4) + i%4 is <= lim.
-#pragma unroll
-                for (int qt = 0; qt < QT; ++qt) {
-                    int lim = p.Sk - 1 - kbase;
-                    if (CAUSAL) lim = min(lim, wq0 + qt * 32 + l32 + p.delta - kbase);
-                    lim -= 4 * hf;
-#pragma unroll
-                    for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i)
-                            if (kt * 32 + 8 * (i >> 2) + (i & 3) > lim) s[qt][kt][i] = kNegInf;
-                }
-            }
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-                float mx = kNegInf;
-#pragma unroll
-                for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[qt][kt][i]);
-                mx = max_xor32(mx);
-                const float mcand = fmaxf(mrow[qt], mx * p.c);
-                if (__any(mcand - mrow[qt] > kRescaleThreshold)) {  // wave-uniform
-                    const float alpha = fast_exp2(mrow[qt] - (mcand == kNegInf ? 0.f : mcand));
-                    mrow[qt] = mcand;
-                    lrow[qt] *= alpha;
-#pragma unroll
-                    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) oacc[qt][dt][i] *= alpha;
-                }
-                const float mbase = (mrow[qt] == kNegInf) ? 0.f : mrow[qt];
-                float ls = lrow[qt];
-#pragma unroll
-                for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-                    for (int half = 0; half < 2; ++half) {
-                        V8 pk;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const float pv = fast_exp2(__builtin_fmaf(s[qt][kt][8 * half + e], p.c, -mbase));
-                            ls += pv;
-                            pk[e] = Elem<T>::from_f32(pv);
-                        }
-                        pb[qt][2 * kt + half] = pk;
-                    }
-                }
-                lrow[qt] = ls;
+            for (int kt = 0; kt < KT; ++kt) {
+                const int r = kt * 32 + l32;
+                const int c = ks * 2 + hf;
+                const V8 a = *reinterpret_cast<const V8*>(Kc + r * D + 8 * (c ^ kswz<D>(r)));
+                s[kt] = Elem<T>::mfma32(a, qf[ks], s[kt]);
             }
         }
-
-        lds_barrier();  // V^T of tile t visible
-
-        if (!wave_skip) {
+        if (need_mask) {
+            // Element i of key tile kt holds key kbase + kt*32 + 8*(i/4) + 4*hf + i%4; it is visible
+            // iff its compile-time offset kt*32 + 8*(i/4) + i%4 is <= lim.
+            int lim = p.Sk - 1 - kbase;
+            if (CAUSAL) lim = min(lim, wq0 + l32 + p.delta - kbase);
+            lim -= 4 * hf;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const int d = dt * 32 + l32;
-                const int sw = vswz(d);
+            for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-                for (int ks = 0; ks < PVS; ++ks) {
-                    const int g1 = ks * 4 + hf, g2 = ks * 4 + 2 + hf;
-                    const u32x2 lo = *reinterpret_cast<const u32x2*>(VTs + d * BN + 4 * (g1 ^ sw));
-                    const u32x2 hi = *reinterpret_cast<const u32x2*>(VTs + d * BN + 4 * (g2 ^ sw));
-                    const u32x4 raw = {lo.x, lo.y, hi.x, hi.y};
-                    const V8 a = __builtin_bit_cast(V8, raw);
+                for (int i = 0; i < 16; ++i)
+                    if (kt * 32 + 8 * (i >> 2) + (i & 3) > lim) s[kt][i] = kNegInf;
+        }
+        float mx = kNegInf;
 #pragma unroll
-                    for (int qt = 0; qt < QT; ++qt) oacc[qt][dt] = Elem<T>::mfma32(a, pb[qt][ks], oacc[qt][dt]);
+        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
+        mx = max_xor32(mx);
+        const float mcand = fmaxf(mrow, mx * p.c);
+        if (__any(mcand - mrow > kRescaleThreshold)) {  // wave-uniform
+            const float alpha = fast_exp2(mrow - (mcand == kNegInf ? 0.f : mcand));
+            mrow = mcand;
+            lrow *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+        }
+        const float mbase = (mrow == kNegInf) ? 0.f : mrow;
+        V8 pb[PVS];
+        float ls = lrow;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                V8 pk;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    // fp32 row sum: a sum of the rounded P would cost up to 2^-9 relative in the LSE of
+                    // rows with few keys
+                    const float pv = fast_exp2(__builtin_fmaf(s[kt][8 * half + e], p.c, -mbase));
+                    ls += pv;
+                    pk[e] = Elem<T>::from_f32(pv);
                 }
+                pb[2 * kt + half] = pk;
+            }
+        }
+        lrow = ls;
+
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const int d = dt * 32 + tr_d;
+#pragma unroll
+            for (int ks = 0; ks < PVS; ++ks) {
+                const int k1 = ks * 16 + tr_k4 + tr_key;  // slots 0-3: keys 16ks + 4hf + j
+                const int k2 = k1 + 8;                    // slots 4-7: keys 16ks + 8 + 4hf + j
+                const V4 lo = __builtin_bit_cast(
+                    V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vc + k1 * D + 8 * ((d >> 3) ^ kswz<D>(k1)) + (d & 7))));
+                const V4 hi = __builtin_bit_cast(
+                    V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vc + k2 * D + 8 * ((d >> 3) ^ kswz<D>(k2)) + (d & 7))));
+                const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                oacc[dt] = Elem<T>::mfma32(a, pb[ks], oacc[dt]);
             }
         }
     };
 
     if (nt > 0) {
-        dma_k(Ksa, 0);
-        load_v(0);
+        dma(Ka, kp, krow, p.ks_s, 0);
+        dma(Va, vp, vrow, p.vs_s, 0);
     }
-    for (int t = 0; t < nt; t += 2) {  // unrolled by two so each tile names its K buffers statically
-        tile(Ksa, Ksb, t);
-        if (t + 1 < nt) tile(Ksb, Ksa, t + 1);
+    // Q fragments (and tile 0) complete here, visibly to the compiler, so that it inserts no load
+    // waits inside the loop (where they would also drain the asynchronous tile loads).
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    for (int t = 0; t < nt; t += 2) {  // unrolled by two so each tile names its buffers statically
+        tile(Ka, Va, Kb, Vb, t);
+        if (t + 1 < nt) tile(Kb, Vb, Ka, Va, t + 1);
     }
 
-    // Epilogue: normalise, stage O through LDS (waves 0-1 in Ksa, 2-3 in Ksb; 16-byte chunk c of
+    // Epilogue: normalise, stage O through LDS (wave w in a 32-row slab of Ka/Kb; 16-byte chunk c of
     // row r at c ^ (r % DCH)) for 16-byte coalesced row stores, and write the LSE.
     __syncthreads();
-    T* Os = (wave < 2 ? Ksa : Ksb) + (wave & 1) * 32 * D;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        const float l = sum_xor32(lrow[qt]);
+    T* Os = (wave < 2 ? Ka : Kb) + (wave & 1) * 32 * D;
+    {
+        const float l = sum_xor32(lrow);
         const float inv = l > 0.f ? 1.f / l : 0.f;
-        const int row = qt * 32 + l32;
+        const int row = l32;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
-                typename Elem<T>::vec4 o4;
+                V4 o4;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o4[e] = Elem<T>::from_f32(oacc[qt][dt][4 * i4 + e] * inv);
+                for (int e = 0; e < 4; ++e) o4[e] = Elem<T>::from_f32(oacc[dt][4 * i4 + e] * inv);
                 const int c = dt * 4 + i4;
-                *reinterpret_cast<typename Elem<T>::vec4*>(Os + row * D + 8 * (c ^ (row % DCH)) + 4 * hf) = o4;
+                *reinterpret_cast<V4*>(Os + row * D + 8 * (c ^ (row % DCH)) + 4 * hf) = o4;
             }
         if (p.lse != nullptr && hf == 0) {
             const int qrow = wq0 + row;
             if (qrow < p.Sq) {
-                const float lse = l > 0.f ? (mrow[qt] + __log2f(l)) * kLn2 : kNegInf;
+                const float lse = l > 0.f ? (mrow + __log2f(l)) * kLn2 : kNegInf;
                 p.lse[b * p.lses_b + hq * p.lses_h + qrow] = lse;
             }
         }
@@ -368,7 +321,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     __syncthreads();
     T* op = reinterpret_cast<T*>(p.o) + b * p.os_b + hq * p.os_h;
 #pragma unroll
-    for (int it = 0; it < QT * 32 * DCH / 64; ++it) {
+    for (int it = 0; it < 32 * DCH / 64; ++it) {
         const int id = it * 64 + lane;
         const int row = id / DCH, c = id % DCH;
         const int qrow = wq0 + row;
