@@ -18,8 +18,8 @@
 //   per-query rescale factor is then a per-lane scalar.
 //
 // LDS: K and V tiles of 64 rows, double-buffered, filled by direct buffer->LDS loads (no VGPR
-// staging); 16-byte chunk c of row r sits at chunk c ^ kswz(r), which keeps the 16-byte K reads and
-// the 8-byte transposed V reads spread over the banks.
+// staging); 16-byte chunk c of row r sits at chunk c ^ kswz(r), which keeps both the 16-byte K reads
+// and the 8-byte transposed V reads free of bank conflicts.
 //
 // Pipeline per key tile j (one barrier per tile):
 //   wait own loads + barrier | K[j+1], V[j+1] -> LDS (async) | S^T = K[j] Q^T | softmax |
@@ -86,9 +86,13 @@ __device__ __forceinline__ BlockCoord block_coord(const PrefillParams& p) {
 // normalisation, which uses the same max for O and l).
 constexpr float kRescaleThreshold = 8.0f;
 
+// XOR swizzle of the 16-byte chunk index of LDS row r (K and V tiles).  It is distinct over any 16
+// consecutive rows (the 16-byte K reads take one chunk of 16 rows per step) and differs above the
+// low two bits for 4 consecutive rows (a transposed V read takes 4 aligned chunks of 4 rows).  With
+// 128-byte rows (D = 64) two rows share a 256-byte bank row, so the pattern is applied per row pair.
 template <int D>
 __device__ __forceinline__ int kswz(int r) {
-    return D >= 128 ? (r & 15) : (r & 7);
+    return D >= 128 ? 4 * (r & 3) + ((r >> 2) & 3) : 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
 }
 
 template <typename T, int D, int QT, bool CAUSAL>
