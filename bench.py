@@ -5,16 +5,21 @@ Step = one causal GQA prefill forward with LSE on the Llama-3-8B attention shape
 S=2048, D=128, bf16), inputs resident in HBM.  ``value`` is algorithmic TFLOP/s (visible pairs only:
 4*B*Hq*D*S(S+1)/2) over the timed steps.  Also reported, each on its own synthetic inputs: split-KV
 decode HBM GB/s (B=64, Hq=32, Hkv=8, D=128, lengths U[512, 8192]), the ring step (4 blocks + LSE
-merge), MMDiT joint attention in bf16 and fp8, and the fp32 causal MHA case.  The CPU baseline is
-libtorch's CPU SDPA (the call SdpaOp::Compute makes on a CPU mesh) on a bounded sample of the same
-prefill, timed on this host, and compared with the GPU output of the same rows.
+merge), MMDiT joint attention in bf16 and fp8, and the fp32-spec causal MHA case.  The CPU baseline is
+libtorch's CPU SDPA in bf16 (the call SdpaOp::Compute makes on a CPU mesh) on the same prefill, timed
+on this host over about ten seconds of repetitions, and compared with the GPU output.
+
+Order: CPU baseline, secondary workloads, then the headline (W warmup steps, K timed steps).  The
+GPU's clocks need some 30 ms of sustained load to settle after idling (measured: back-to-back prefill
+launches rise from ~610 to ~925 TFLOP/s over the first 30 ms), so the headline runs last, after GPU
+work, and every secondary measurement first runs its workload for 0.15 s untimed.
 
 Prints ONE JSON line on stdout; human-readable detail goes to stderr.
 """
 import argparse
 import json
-import math
 import os
+import re
 import sys
 import time
 
@@ -28,6 +33,10 @@ PEAK_BF16 = 2.5e15   # MI355X dense bf16 MFMA, FLOP/s (published)
 PEAK_FP8 = 5.0e15    # MI355X dense fp8 MFMA
 PEAK_HBM = 8.0e12    # MI355X HBM3E, B/s
 
+# HBM bytes per launch of the headline kernel, from the two calibrated rocprofv3 --pmc runs
+# (FETCH_SIZE, WRITE_SIZE) summarised in this file.
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "prefill_fwd_causal_gqa_b4_s2048_traffic.md")
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -37,16 +46,31 @@ def causal_flops(B, Hq, S, D):
     return 4 * B * Hq * D * S * (S + 1) // 2
 
 
+def profiled_traffic():
+    """traffic_bytes_per_launch from the committed profile summary, or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
 class Timer:
     """HIP events on the stream the kernels launch on (torch's current stream)."""
 
     def __init__(self, torch):
         self.torch = torch
 
-    def run(self, fn, reps, warmup=2, flush=None):
+    def run(self, fn, reps, settle=0.15, flush=None):
         t = self.torch
-        for _ in range(warmup):
+        t0 = time.perf_counter()
+        n = 0
+        while n < 2 or time.perf_counter() - t0 < settle:
             fn()
+            n += 1
+            if n % 8 == 0:
+                t.cuda.synchronize()
         t.cuda.synchronize()
         times = []
         for _ in range(reps):
@@ -61,13 +85,118 @@ class Timer:
         return float(np.median(times)), float(np.mean(times))
 
 
+def cpu_baseline(torch, qn, kn, vn, min_seconds):
+    """libtorch CPU SDPA (bf16, all threads) on the full headline workload, repeated for min_seconds."""
+    from oracle import dtorch_cpu_path as cpu
+
+    threads = torch.get_num_threads()
+    q, k, v = (torch.from_numpy(x).to(torch.bfloat16) for x in (qn, kn, vn))
+    B, Hq, S, D = q.shape
+    out = cpu.sdpa(q, k, v, is_causal=True, enable_gqa=True)  # warm-up, and the reference output
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3 or time.perf_counter() - t0 < min_seconds:
+        cpu.sdpa(q, k, v, is_causal=True, enable_gqa=True)
+        reps += 1
+    dt = time.perf_counter() - t0
+    rate = causal_flops(B, Hq, S, D) * reps / dt
+    info = {
+        "value": round(rate / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+        "sample": f"libtorch CPU SDPA in bf16 (SdpaOp::Compute's call on a CPU mesh) on the whole workload "
+                  f"(B={B}, Hq={Hq}, Hkv={k.shape[1]}, S={S}, D={D}, causal, GQA), {reps} repetitions in "
+                  f"{dt:.1f} s on {threads} threads; host: {_physical_cores()} physical cores, "
+                  f"{os.cpu_count()} logical CPUs",
+    }
+    log(f"CPU baseline: {rate / 1e12:.3f} TFLOP/s on {threads} threads ({reps} reps, {dt:.1f} s)")
+    return info, out
+
+
+def secondary_workloads(torch, F, dev, timer):
+    extras = {}
+    flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+
+    def flush():
+        flush_buf.zero_()
+
+    # split-KV decode
+    Bd, Hqd, Hkvd, Smax, Dd = 64, 32, 8, 8192, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    qd = torch.randn(Bd, Hqd, 1, Dd, device=dev, generator=g).to(torch.bfloat16)
+    kc = torch.randn(Bd, Hkvd, Smax, Dd, device=dev, generator=g).to(torch.bfloat16)
+    vc = torch.randn(Bd, Hkvd, Smax, Dd, device=dev, generator=g).to(torch.bfloat16)
+    lens_np = np.random.default_rng(0).integers(512, 8192, size=Bd, endpoint=True).astype(np.int32)
+    lens = torch.from_numpy(lens_np).to(dev)
+    tot = int(lens_np.sum())
+    dbytes = 4096 * tot + Bd * Hqd * Dd * 2 * 2 + Bd * Hqd * 4
+    med, _ = timer.run(lambda: F.decode_attention(qd, kc, vc, lens), reps=20, flush=flush)
+    gbs = dbytes / med / 1e9
+    extras["decode_c3"] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs * 1e9 / PEAK_HBM, 4),
+                           "us": round(med * 1e6, 1), "bytes": dbytes, "sum_len": tot,
+                           "note": "L2/MALL flushed before every rep"}
+    log(f"decode B=64 Hq=32 Hkv=8 lengths U[512,8192]: {med * 1e6:.1f} us, {gbs:.0f} GB/s "
+        f"({100 * gbs * 1e9 / PEAK_HBM:.1f}% of HBM)")
+    del kc, vc, qd
+
+    # ring step: 4 blocks (1 causal diagonal + 3 full) + merge
+    C = 4096
+    q4 = torch.randn(1, 32, C, 128, device=dev, generator=g).to(torch.bfloat16)
+    k4 = [torch.randn(1, 8, C, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(4)]
+    v4 = [torch.randn(1, 8, C, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(4)]
+    blocks = []
+
+    def ring_blocks():
+        blocks.clear()
+        for c in range(4):
+            blocks.append(F.scaled_dot_product_attention_with_lse(
+                q4, k4[c], v4[c], is_causal=(c == 3), enable_gqa=True, q_offset=3 * C, k_offset=c * C))
+
+    rflops = 3 * (4 * 32 * 128 * C * C) + causal_flops(1, 32, C, 128)
+    med, _ = timer.run(ring_blocks, reps=5)
+    extras["ring_c4_blocks"] = {"TFLOP/s": round(rflops / med / 1e12, 1),
+                                "frac_bf16": round(rflops / med / PEAK_BF16, 4), "ms": round(med * 1e3, 3)}
+    mbytes = 5 * (32 * C * 128 * 2 + 32 * C * 4)
+    med_m, _ = timer.run(lambda: F.lse_merge([b[0] for b in blocks], [b[1] for b in blocks]), reps=20,
+                         flush=flush)
+    extras["ring_c4_merge"] = {"GB/s": round(mbytes / med_m / 1e9, 1),
+                               "frac_hbm": round(mbytes / med_m / PEAK_HBM, 4), "us": round(med_m * 1e6, 1)}
+    log(f"ring step 4x4096: blocks {med * 1e3:.3f} ms ({rflops / med / 1e12:.0f} TFLOP/s), merge "
+        f"{med_m * 1e6:.1f} us ({mbytes / med_m / 1e9:.0f} GB/s)")
+    del q4, k4, v4, blocks
+
+    # MMDiT joint attention, bf16 and fp8
+    q5, k5, v5 = (torch.randn(1, 24, 4608, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    f5 = 4 * 24 * 128 * 4608 * 4608
+    med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5), reps=10)
+    extras["mmdit_c5a_bf16"] = {"TFLOP/s": round(f5 / med / 1e12, 1), "frac_bf16": round(f5 / med / PEAK_BF16, 4),
+                                "us": round(med * 1e6, 1)}
+    opt = F.SdpaOption(sage_attn_type="native_fp8")
+    med8, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5, sdpa_option=opt), reps=10)
+    med_q, _ = timer.run(lambda: [F.quantize_fp8_per_head(x) for x in (q5, k5, v5)], reps=10)
+    kern8 = max(med8 - med_q, 1e-9)
+    extras["mmdit_c5b_fp8"] = {"TFLOP/s_end_to_end": round(f5 / med8 / 1e12, 1),
+                               "TFLOP/s_attention_kernel": round(f5 / kern8 / 1e12, 1),
+                               "frac_fp8_kernel": round(f5 / kern8 / PEAK_FP8, 4),
+                               "quantize_us": round(med_q * 1e6, 1), "us": round(med8 * 1e6, 1)}
+    log(f"MMDiT 1x24x4608: bf16 {f5 / med / 1e12:.0f} TFLOP/s; fp8 end-to-end {f5 / med8 / 1e12:.0f} TFLOP/s "
+        f"(quantize {med_q * 1e6:.0f} us, attention ~{f5 / kern8 / 1e12:.0f} TFLOP/s)")
+    del q5, k5, v5
+
+    # fp32-spec causal MHA (runs in bf16 on the GPU)
+    q1, k1, v1 = (torch.randn(1, 8, 512, 64, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    f1 = causal_flops(1, 8, 512, 64)
+    med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q1, k1, v1, is_causal=True), reps=20)
+    extras["c1_causal_mha_d64"] = {"TFLOP/s": round(f1 / med / 1e12, 2), "us": round(med * 1e6, 1)}
+    del flush_buf
+    return extras
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-extras", action="store_true", help="only the headline prefill")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="length of the CPU baseline sample")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 device copies of 1 GiB (known traffic) to scale rocprof byte counters")
     args = ap.parse_args()
@@ -94,20 +223,26 @@ def main():
         del src, dst
         log("copy calibration: 3 x copy of 1 GiB (1,048,576 KiB read and written per launch)")
 
-    # ---------------------------------------------------------------- headline: Llama prefill
+    # headline inputs: Llama-3-8B attention shape
     B, Hq, Hkv, S, D = 4, 32, 8, 2048, 128
     rng = np.random.default_rng(0)
     qn = rng.standard_normal((B, Hq, S, D), dtype=np.float32)
     kn = rng.standard_normal((B, Hkv, S, D), dtype=np.float32)
     vn = rng.standard_normal((B, Hkv, S, D), dtype=np.float32)
-    q, k, v = (torch.from_numpy(x).to(torch.bfloat16).to(dev) for x in (qn, kn, vn))
     flops = causal_flops(B, Hq, S, D)
+
+    cpu_info, cpu_out = (None, None) if args.no_cpu else cpu_baseline(torch, qn, kn, vn, args.cpu_seconds)
+    extras = {} if args.no_extras else secondary_workloads(torch, F, dev, timer)
+
+    # ---------------------------------------------------------------- headline: W warmup, K timed steps
+    q, k, v = (torch.from_numpy(x).to(torch.bfloat16).to(dev) for x in (qn, kn, vn))
 
     def step():
         return F.scaled_dot_product_attention_with_lse(q, k, v, is_causal=True, enable_gqa=True)
 
+    out = None
     for _ in range(args.warmup):
-        step()
+        out = step()
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     t0 = time.perf_counter()
@@ -122,8 +257,8 @@ def main():
     value = flops / (wall / args.steps) / 1e12
     k_avg = float(np.mean(kern))
     achieved = flops / k_avg / 1e12
-    log(f"C2 prefill causal GQA bf16: {ms_per_step:.3f} ms/step wall, kernel avg {k_avg * 1e6:.1f} us -> "
-        f"{achieved:.1f} TFLOP/s ({100 * achieved * 1e12 / PEAK_BF16:.1f}% of bf16 peak)")
+    log(f"prefill causal GQA B=4 Hq=32 Hkv=8 S=2048 D=128 bf16: {ms_per_step:.3f} ms/step wall, kernel avg "
+        f"{k_avg * 1e6:.1f} us -> {achieved:.1f} TFLOP/s ({100 * achieved * 1e12 / PEAK_BF16:.1f}% of bf16 peak)")
 
     result = {
         "metric": "prefill attn TFLOP/s (MFMA util %) + decode attn HBM GB/s, 1xMI355X",
@@ -137,130 +272,20 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: N(0,1) from numpy default_rng(0), cast to bf16 (extras: torch.randn on device)",
+        "data": "synthetic: N(0,1) from numpy default_rng(0), cast to bf16 (secondary workloads: torch.randn "
+                "on the device)",
         "config": {"workload": "Llama-3-8B-shape causal GQA prefill attention with LSE", "B": B, "Hq": Hq,
                    "Hkv": Hkv, "S": S, "D": D, "causal": True, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": None,
+                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": profiled_traffic(),
                      "kernel": "prefill_fwd_kernel<bf16,128,1,causal>",
-                     "work_per_launch": f"{flops} FLOP (4*B*Hq*D*S(S+1)/2)"},
+                     "work_per_launch": f"{flops} FLOP (4*B*Hq*D*S(S+1)/2)",
+                     "avg_launch_us": round(k_avg * 1e6, 2)},
     }
-    del step
-
-    extras = {}
-    if not args.no_extras:
-        flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-
-        def flush():
-            flush_buf.zero_()
-
-        # C3 decode
-        Bd, Hqd, Hkvd, Smax, Dd = 64, 32, 8, 8192, 128
-        g = torch.Generator(device=dev).manual_seed(0)
-        qd = torch.randn(Bd, Hqd, 1, Dd, device=dev, generator=g).to(torch.bfloat16)
-        kc = torch.randn(Bd, Hkvd, Smax, Dd, device=dev, generator=g).to(torch.bfloat16)
-        vc = torch.randn(Bd, Hkvd, Smax, Dd, device=dev, generator=g).to(torch.bfloat16)
-        lens_np = np.random.default_rng(0).integers(512, 8192, size=Bd, endpoint=True).astype(np.int32)
-        lens = torch.from_numpy(lens_np).to(dev)
-        tot = int(lens_np.sum())
-        dbytes = 4096 * tot + Bd * Hqd * Dd * 2 * 2 + Bd * Hqd * 4
-        med, mean = timer.run(lambda: F.decode_attention(qd, kc, vc, lens), reps=20, flush=flush)
-        gbs = dbytes / med / 1e9
-        extras["decode_c3"] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs * 1e9 / PEAK_HBM, 4),
-                               "us": round(med * 1e6, 1), "bytes": dbytes, "sum_len": tot}
-        log(f"C3 decode: {med * 1e6:.1f} us, {gbs:.0f} GB/s ({100 * gbs * 1e9 / PEAK_HBM:.1f}% of HBM)")
-        del kc, vc, qd
-
-        # C4 ring step: 4 blocks (1 causal diagonal + 3 full) + merge
-        C = 4096
-        q4 = torch.randn(1, 32, C, 128, device=dev, generator=g).to(torch.bfloat16)
-        k4 = [torch.randn(1, 8, C, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(4)]
-        v4 = [torch.randn(1, 8, C, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(4)]
-        blocks = []
-
-        def ring_blocks():
-            blocks.clear()
-            for c in range(4):
-                blocks.append(F.scaled_dot_product_attention_with_lse(
-                    q4, k4[c], v4[c], is_causal=(c == 3), enable_gqa=True, q_offset=3 * C, k_offset=c * C))
-
-        rflops = 3 * (4 * 32 * 128 * C * C) + causal_flops(1, 32, C, 128)
-        med, _ = timer.run(ring_blocks, reps=5)
-        extras["ring_c4_blocks"] = {"TFLOP/s": round(rflops / med / 1e12, 1),
-                                    "frac_bf16": round(rflops / med / PEAK_BF16, 4), "ms": round(med * 1e3, 3)}
-        mbytes = 5 * (32 * C * 128 * 2 + 32 * C * 4)
-        med_m, _ = timer.run(lambda: F.lse_merge([b[0] for b in blocks], [b[1] for b in blocks]), reps=20,
-                             flush=flush)
-        extras["ring_c4_merge"] = {"GB/s": round(mbytes / med_m / 1e9, 1),
-                                   "frac_hbm": round(mbytes / med_m / PEAK_HBM, 4), "us": round(med_m * 1e6, 1)}
-        log(f"C4 ring: blocks {med * 1e3:.3f} ms ({rflops / med / 1e12:.0f} TFLOP/s), merge {med_m * 1e6:.1f} us "
-            f"({mbytes / med_m / 1e9:.0f} GB/s)")
-        del q4, k4, v4, blocks
-
-        # C5 MMDiT joint attention, bf16 and fp8
-        q5, k5, v5 = (torch.randn(1, 24, 4608, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
-        f5 = 4 * 24 * 128 * 4608 * 4608
-        med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5), reps=10)
-        extras["mmdit_c5a_bf16"] = {"TFLOP/s": round(f5 / med / 1e12, 1), "frac_bf16": round(f5 / med / PEAK_BF16, 4),
-                                    "us": round(med * 1e6, 1)}
-        opt = F.SdpaOption(sage_attn_type="native_fp8")
-        med8, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5, sdpa_option=opt), reps=10)
-        med_q, _ = timer.run(lambda: [F.quantize_fp8_per_head(x) for x in (q5, k5, v5)], reps=10)
-        kern8 = max(med8 - med_q, 1e-9)
-        extras["mmdit_c5b_fp8"] = {"TFLOP/s_end_to_end": round(f5 / med8 / 1e12, 1),
-                                   "TFLOP/s_attention_kernel": round(f5 / kern8 / 1e12, 1),
-                                   "frac_fp8_kernel": round(f5 / kern8 / PEAK_FP8, 4),
-                                   "quantize_us": round(med_q * 1e6, 1), "us": round(med8 * 1e6, 1)}
-        log(f"C5 MMDiT: bf16 {f5 / med / 1e12:.0f} TFLOP/s; fp8 end-to-end {f5 / med8 / 1e12:.0f} TFLOP/s "
-            f"(quantize {med_q * 1e6:.0f} us, attention ~{f5 / kern8 / 1e12:.0f} TFLOP/s)")
-        del q5, k5, v5
-
-        # C1 fp32-spec causal MHA (runs in bf16 on the GPU)
-        q1, k1, v1 = (torch.randn(1, 8, 512, 64, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
-        f1 = causal_flops(1, 8, 512, 64)
-        med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q1, k1, v1, is_causal=True), reps=20)
-        extras["c1_causal_mha_d64"] = {"TFLOP/s": round(f1 / med / 1e12, 2), "us": round(med * 1e6, 1)}
-        del flush_buf
+    if cpu_info is not None:
+        cpu_info["gpu_vs_cpu_max_abs_err"] = round(float((out[0].float().cpu() - cpu_out.float()).abs().max()), 5)
+        result["cpu_baseline"] = cpu_info
     result["extras"] = extras
-
-    # ---------------------------------------------------------------- CPU baseline (libtorch CPU SDPA)
-    if not args.no_cpu:
-        from oracle import dtorch_cpu_path as cpu
-
-        threads = os.cpu_count() or 1
-        torch.set_num_threads(threads)
-        o_gpu = out[0]
-        # bounded sample: batch 0, the first `nh` query heads (kv heads follow), all 2048 rows
-        def cpu_run(nh):
-            nkv = max(1, nh // (Hq // Hkv))
-            tq = torch.from_numpy(qn[:1, :nh]).to(torch.bfloat16).float()
-            tk = torch.from_numpy(kn[:1, :nkv]).to(torch.bfloat16).float()
-            tv = torch.from_numpy(vn[:1, :nkv]).to(torch.bfloat16).float()
-            t0 = time.perf_counter()
-            r = cpu.sdpa(tq, tk, tv, is_causal=True, enable_gqa=True)
-            return time.perf_counter() - t0, r
-
-        dt1, _ = cpu_run(4)  # warmup + estimate
-        per_head = dt1 / 4
-        nh = int(min(Hq, max(4, (5.0 / max(per_head, 1e-6)) // 4 * 4)))
-        times = []
-        ref = None
-        for _ in range(3):
-            dt, ref = cpu_run(nh)
-            times.append(dt)
-        dt = float(np.median(times))
-        sflops = causal_flops(1, nh, S, D)
-        err = float((o_gpu[:1, :nh].float().cpu() - ref).abs().max())
-        result["cpu_baseline"] = {
-            "value": round(sflops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
-            "sample": f"libtorch CPU SDPA fp32 (SdpaOp::Compute's call on a CPU mesh) on batch 0, {nh} of 32 query "
-                      f"heads, S=2048, causal, GQA; median of 3 reps, {dt:.2f} s each; physical cores "
-                      f"{_physical_cores()}, logical CPUs {os.cpu_count()}",
-            "gpu_vs_cpu_max_abs_err": round(err, 5),
-        }
-        log(f"CPU baseline: {sflops / dt / 1e12:.3f} TFLOP/s on {threads} threads ({nh} heads, {dt:.2f} s); "
-            f"GPU vs CPU max-abs {err:.2e}")
-
     print(json.dumps(result), flush=True)
 
 
