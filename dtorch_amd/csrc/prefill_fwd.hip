@@ -121,7 +121,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS bases stay scalar
     const int l32 = lane & 31;
     const int hf = lane >> 5;
 
@@ -208,16 +208,19 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
         for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
+        __builtin_amdgcn_s_setprio(1);
+        // key tile kt=0 completes first, so its row max can overlap the MFMAs of kt=1
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
+        for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
-            for (int kt = 0; kt < KT; ++kt) {
+            for (int ks = 0; ks < KSTEPS; ++ks) {
                 const int r = kt * 32 + l32;
                 const int c = ks * 2 + hf;
                 const V8 a = *reinterpret_cast<const V8*>(Kc + r * D + 8 * (c ^ kswz<D>(r)));
                 s[kt] = Elem<T>::mfma32(a, qf[ks], s[kt]);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         if (need_mask) {
             // Element i of key tile kt holds key kbase + kt*32 + 8*(i/4) + 4*hf + i%4; it is visible
             // iff its compile-time offset kt*32 + 8*(i/4) + i%4 is <= lim.
@@ -246,6 +249,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
 #pragma unroll
                 for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
         }
+        __builtin_amdgcn_s_setprio(1);
         const float mbase = (mrow == kNegInf) ? 0.f : mrow;
         V8 pb[PVS];
         float ls = lrow;
@@ -267,11 +271,13 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
         }
         lrow = ls;
 
+        // k-step outer: the four MFMAs of step ks need only P chunk ks, so they can run while the
+        // exponentials of the later chunks are still being computed
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            const int d = dt * 32 + tr_d;
+        for (int ks = 0; ks < PVS; ++ks) {
 #pragma unroll
-            for (int ks = 0; ks < PVS; ++ks) {
+            for (int dt = 0; dt < DT; ++dt) {
+                const int d = dt * 32 + tr_d;
                 const int k1 = ks * 16 + tr_k4 + tr_key;  // slots 0-3: keys 16ks + 4hf + j
                 const int k2 = k1 + 8;                    // slots 4-7: keys 16ks + 8 + 4hf + j
                 const V4 lo = __builtin_bit_cast(
@@ -282,6 +288,19 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
                 oacc[dt] = Elem<T>::mfma32(a, pb[ks], oacc[dt]);
             }
         }
+        // Issue order of this block: the V^T reads of step 0 and P chunk 0, then each PV MFMA
+        // followed by two V^T reads and a slice of the next chunk's exponentials.
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * DT, 0);
+        __builtin_amdgcn_sched_group_barrier(0x402, 28, 0);
+#pragma unroll
+        for (int i = 0; i < (PVS - 1) * DT; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x402, 7, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < DT; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_s_setprio(0);
     };
 
     if (nt > 0) {
