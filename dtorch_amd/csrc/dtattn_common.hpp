@@ -225,6 +225,41 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // Wait until this wave's global loads, including direct global->LDS loads, have completed.
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// ---- workgroup placement ------------------------------------------------------------------------
+
+// Workgroup -> (query block, batch, query head, kv head) of the prefill kernels.  Causal launches take
+// the longest query blocks first.  Workgroups are dispatched round-robin over the 8 XCDs
+// (blockIdx % 8), each with its own L2; with xcd_map the slices (b, kv head) are dealt to XCDs so that
+// every workgroup reading a slice's K/V runs on the same XCD and the slice is fetched from HBM once per
+// L2 instead of once per XCD.  xcd_map requires B * Hkv to be a multiple of 8.
+struct BlockCoord {
+    int qb, b, hq, hk;
+};
+
+template <bool CAUSAL>
+__device__ __forceinline__ BlockCoord block_coord(int B, int Hq, int Hkv, int group, int n_qblocks, int xcd_map) {
+    const int bid = blockIdx.x;
+    BlockCoord r;
+    if (xcd_map) {
+        const int x = bid & 7, j = bid >> 3;
+        const int per_rank = (B * Hkv / 8) * group;  // workgroups per query-block rank per XCD
+        const int rank = j / per_rank, rem = j % per_rank;
+        const int slice = (rem / group) * 8 + x;
+        r.b = slice / Hkv;
+        r.hk = slice % Hkv;
+        r.hq = r.hk * group + rem % group;
+        r.qb = CAUSAL ? (n_qblocks - 1 - rank) : rank;
+    } else {
+        const int bh = B * Hq;
+        const int rest = bid % bh;
+        r.qb = CAUSAL ? (n_qblocks - 1 - bid / bh) : (bid / bh);
+        r.hq = rest % Hq;
+        r.b = rest / Hq;
+        r.hk = r.hq / group;
+    }
+    return r;
+}
+
 // ---- host-side status plumbing ----------------------------------------------------------------
 
 void set_last_error(const char* fmt, ...);

@@ -49,36 +49,9 @@ struct PrefillParams {
     int32_t xcd_map;  // 1: group the workgroups of each (batch, kv head) slice on one XCD
 };
 
-// Workgroup -> (query block, batch, query head).  Causal launches take the longest query blocks
-// first.  Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8), each with its own L2;
-// with xcd_map the slices (b, kv head) are dealt to XCDs so that every workgroup reading a slice's
-// K/V runs on the same XCD and the slice is fetched from HBM once per L2 instead of once per XCD.
-struct BlockCoord {
-    int qb, b, hq, hk;
-};
-
 template <bool CAUSAL>
 __device__ __forceinline__ BlockCoord block_coord(const PrefillParams& p) {
-    const int bid = blockIdx.x;
-    BlockCoord r;
-    if (p.xcd_map) {
-        const int x = bid & 7, j = bid >> 3;
-        const int per_rank = (p.B * p.Hkv / 8) * p.group;  // workgroups per query-block rank per XCD
-        const int rank = j / per_rank, rem = j % per_rank;
-        const int slice = (rem / p.group) * 8 + x;
-        r.b = slice / p.Hkv;
-        r.hk = slice % p.Hkv;
-        r.hq = r.hk * p.group + rem % p.group;
-        r.qb = CAUSAL ? (p.n_qblocks - 1 - rank) : rank;
-    } else {
-        const int bh = p.B * p.Hq;
-        const int rest = bid % bh;
-        r.qb = CAUSAL ? (p.n_qblocks - 1 - bid / bh) : (bid / bh);
-        r.hq = rest % p.Hq;
-        r.b = rest / p.Hq;
-        r.hk = r.hq / p.group;
-    }
-    return r;
+    return block_coord<CAUSAL>(p.B, p.Hq, p.Hkv, p.group, p.n_qblocks, p.xcd_map);
 }
 
 // Lazy rescaling: the running max only moves (and O, l are only rescaled) when some row's max grew
