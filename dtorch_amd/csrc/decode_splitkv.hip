@@ -240,10 +240,25 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p)
     float acc[DPL];
 #pragma unroll
     for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
-    for (int s = 0; s < ns; ++s) {
-        const float w = __expf(pl[s] - mx) / sum;
+    const float inv = 1.f / sum;
+    // batches of MB partials: every load of a batch is issued before the first is used, so the
+    // wave waits for one memory latency per batch instead of one per partial
+    constexpr int MB = 8;
+    for (int s0 = 0; s0 < ns; s0 += MB) {
+        float lw[MB], v[MB][DPL];
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(w, po[(int64_t)s * D + lane * DPL + e], acc[e]);
+        for (int j = 0; j < MB; ++j) {
+            const int s = min(s0 + j, ns - 1);  // clamped: in bounds, weight zeroed below
+            lw[j] = pl[s];
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) v[j][e] = po[(int64_t)s * D + lane * DPL + e];
+        }
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+            const float w = s0 + j < ns ? __expf(lw[j] - mx) * inv : 0.f;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) acc[e] = __builtin_fmaf(w, v[j][e], acc[e]);
+        }
     }
     T* op = reinterpret_cast<T*>(p.o) + b * p.os_b + hq * p.os_h;
 #pragma unroll
