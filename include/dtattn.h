@@ -89,7 +89,7 @@ typedef struct {
     const void* q;         /* [B, Hq, 1, D] */
     const void* k_cache;   /* [B, Hkv, S_max, D] */
     const void* v_cache;   /* [B, Hkv, S_max, D] */
-    const int32_t* lengths;/* [B] device int32, 1 <= lengths[b] <= S_max */
+    const int32_t* lengths;/* [B] device int32; clamped to [0, S_max]; 0 gives O = 0, LSE = -inf */
     void* o;               /* [B, Hq, 1, D], same dtype as q */
     float* lse;            /* [B, Hq] fp32; may be NULL */
     int64_t B, Hq, Hkv, S_max, D;
@@ -100,7 +100,7 @@ typedef struct {
     int64_t lse_stride[1]; /* B (H stride is 1) */
     int32_t dtype;         /* BF16 or FP16 */
     float scale;           /* <= 0 means 1/sqrt(D) */
-    int32_t chunk;         /* tokens per split, multiple of 64; 0 picks the default (256) */
+    int32_t chunk;         /* tokens per split: 128, 256 or 512; 0 picks the default (128) */
     void* workspace;       /* >= dtattn_decode_workspace_size(...) bytes, 256-byte aligned */
     size_t workspace_bytes;
 } dtattn_decode_args;

@@ -79,3 +79,27 @@ def test_config5b_mmdit_fp8_full_size():
         ro, rl = orc.sdpa_fwd(rounded(q[0, h])[None], rounded(k[0, h])[None], rounded(v[0, h])[None])
         assert max_abs(o[0, h], ro[0]) <= O_TOL_FP8, h
         assert lse_rel(lse[0, h], rl[0]) <= 5e-2, h
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_fp8_gqa_causal_offsets_ragged(D):
+    # GQA group 4, Sq != Sk with the causal rule j + k_offset <= i + q_offset, ragged tails on both
+    # sides (the key permutation of the score MFMA and the tail mask meet here), and a q_offset that
+    # leaves the first rows fully masked (O = 0, LSE = -inf).
+    rng = np.random.default_rng(11)
+    B, Hq, Hkv, Sq, Sk = 2, 8, 2, 200, 333
+    q, k, v = randn(rng, (B, Hq, Sq, D)), randn(rng, (B, Hkv, Sk, D)), randn(rng, (B, Hkv, Sk, D))
+    F = _F()
+    opt = F.SdpaOption(sage_attn_type="native_fp8")
+    deq = [orc.fp8_dequantize_per_head(*orc.fp8_quantize_per_head(rounded(x).astype(np.float32))) for x in (q, k, v)]
+    for q_off, k_off in ((133, 0), (0, 40)):
+        o, lse = F.scaled_dot_product_attention_with_lse(to_dev(q), to_dev(k), to_dev(v), is_causal=True,
+                                                         enable_gqa=True, q_offset=q_off, k_offset=k_off,
+                                                         sdpa_option=opt)
+        torch.cuda.synchronize()
+        o, lse = host(o), host(lse)
+        do, dl = orc.sdpa_fwd(*deq, is_causal=True, enable_gqa=True, q_offset=q_off, k_offset=k_off)
+        assert max_abs(o, do) <= O_TOL_FP8, (q_off, k_off)
+        visible = np.isfinite(dl)
+        assert lse_rel(lse[visible], dl[visible]) <= LSE_TOL, (q_off, k_off)
+        assert np.all(np.isneginf(lse[~visible])) and np.all(o[~visible] == 0), (q_off, k_off)
