@@ -193,6 +193,14 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
                 s[kt] = Elem<T>::mfma32(a, qf[ks], s[kt]);
             }
         }
+        // K fragment reads run 4 MFMAs ahead of their use
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < KT * KSTEPS - 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         __builtin_amdgcn_s_setprio(0);
         if (need_mask) {
             // Element i of key tile kt holds key kbase + kt*32 + 8*(i/4) + 4*hf + i%4; it is visible
@@ -263,7 +271,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
         }
         // Issue order of this block: the V^T reads of step 0 and P chunk 0, then each PV MFMA
         // followed by two V^T reads and a slice of the next chunk's exponentials.
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * DT, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4 * DT, 0);
         __builtin_amdgcn_sched_group_barrier(0x402, 28, 0);
 #pragma unroll
         for (int i = 0; i < (PVS - 1) * DT; ++i) {
