@@ -115,8 +115,8 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int tl = wave * TPW + sb * SB + i * TPI + tsub;
-            kr[i] = buf_ld16(krs, (uint32_t)(tl * kpitch + c8 * 16));
-            vr[i] = buf_ld16(vrs, (uint32_t)(tl * vpitch + c8 * 16));
+            kr[i] = buf_ld16_nt(krs, (uint32_t)(tl * kpitch + c8 * 16));  // the cache is read once per call
+            vr[i] = buf_ld16_nt(vrs, (uint32_t)(tl * vpitch + c8 * 16));
         }
         float sc[NI][G];
 #pragma unroll

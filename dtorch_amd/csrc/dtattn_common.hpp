@@ -98,6 +98,10 @@ __device__ __forceinline__ uint32_t pack2(float x, float y) {
 // ---- raw memory access ------------------------------------------------------------------------
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// Same load with the non-temporal hint, for data read exactly once.
+__device__ __forceinline__ u32x4 ld16_nt(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 // Buffer resource over `bytes` bytes from `base` (raw, stride 0).  Loads at offsets >= bytes return
@@ -109,6 +113,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // 16-byte load through a buffer resource (voffset in bytes).
 __device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0));
+}
+
+// 16-byte load with the non-temporal hint (cache policy NT): for data streamed exactly once, such as
+// a KV cache in decode, so that it does not evict reused lines from L2.
+__device__ __forceinline__ u32x4 buf_ld16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 2));
 }
 
 // 16 bytes per lane straight into LDS: lane l lands at lds + 16 * l (lds is wave-uniform).

@@ -22,20 +22,21 @@ struct MergeParams {
     int32_t H, S, n;
 };
 
+// Block outputs are read exactly once: non-temporal loads.
 template <typename TI>
 __device__ __forceinline__ void load8(const TI* p, float* out);
 template <>
 __device__ __forceinline__ void load8<bf16_t>(const bf16_t* p, float* out) {
-    unpack8<bf16_t>(ld16(p), out);
+    unpack8<bf16_t>(ld16_nt(p), out);
 }
 template <>
 __device__ __forceinline__ void load8<f16_t>(const f16_t* p, float* out) {
-    unpack8<f16_t>(ld16(p), out);
+    unpack8<f16_t>(ld16_nt(p), out);
 }
 template <>
 __device__ __forceinline__ void load8<float>(const float* p, float* out) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+    const f32x4 a = __builtin_bit_cast(f32x4, ld16_nt(p));
+    const f32x4 b = __builtin_bit_cast(f32x4, ld16_nt(p + 4));
     out[0] = a.x, out[1] = a.y, out[2] = a.z, out[3] = a.w;
     out[4] = b.x, out[5] = b.y, out[6] = b.z, out[7] = b.w;
 }
