@@ -192,3 +192,21 @@ def _causal_rows(q, k, v, qpos):
     p = np.exp(logits - m)
     s = p.sum(-1, keepdims=True)
     return (p @ v) / s, (m + np.log(s))[:, 0]
+
+
+def test_decode_zero_length_sequences():
+    # lengths of 0 (and lengths clamped to S_max) are defined: an empty sequence gives O = 0, LSE = -inf;
+    # the other sequences of the batch are unaffected
+    rng = np.random.default_rng(9)
+    B, Hq, Hkv, Smax, D = 4, 8, 2, 300, 128
+    q, kc, vc = randn(rng, (B, Hq, 1, D)), randn(rng, (B, Hkv, Smax, D)), randn(rng, (B, Hkv, Smax, D))
+    lengths = np.array([0, 300, 0, 130], dtype=np.int32)
+    F = _F()
+    o, lse = F.decode_attention(to_dev(q), to_dev(kc), to_dev(vc), torch.from_numpy(lengths).cuda())
+    torch.cuda.synchronize()
+    o, lse = host(o), host(lse)
+    for b in (0, 2):
+        assert np.all(o[b] == 0) and np.all(np.isneginf(lse[b])), b
+    ro, rl = orc.decode(rounded(q[[1, 3]]), rounded(kc[[1, 3]]), rounded(vc[[1, 3]]), lengths[[1, 3]])
+    assert max_abs(o[[1, 3]], ro) <= O_TOL_BF16
+    assert lse_rel(lse[[1, 3]], rl[..., 0]) <= LSE_TOL

@@ -162,3 +162,15 @@ def test_config5a_mmdit_joint_full_size():
     o, lse = F.scaled_dot_product_attention_with_lse(to_dev(q), to_dev(k), to_dev(v))
     torch.cuda.synchronize()
     _sampled_check(o, lse, q, k, v, [(0, 0), (0, 11), (0, 23)], False)
+
+
+def test_prefill_empty_key_set():
+    # Sk = 0: every row is fully masked (O = 0, LSE = -inf), with and without causal masking
+    F = _F()
+    q = torch.randn(1, 4, 70, 128, device="cuda", dtype=torch.bfloat16)
+    kv = torch.empty(1, 2, 0, 128, device="cuda", dtype=torch.bfloat16)
+    for causal in (False, True):
+        o, lse = F.scaled_dot_product_attention_with_lse(q, kv, kv, is_causal=causal, enable_gqa=True)
+        torch.cuda.synchronize()
+        assert o.shape == q.shape and lse.shape == (1, 4, 70)
+        assert bool((o == 0).all()) and bool(torch.isneginf(lse).all())
