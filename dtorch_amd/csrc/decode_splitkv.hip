@@ -33,9 +33,14 @@ struct DecodeParams {
     int64_t vs_b, vs_h, vs_s;
     int64_t os_b, os_h;
     int64_t lses_b;
-    int32_t B, Hq, Hkv, S_max, group, sub;  // sub = heads handled per workgroup
+    int32_t B, Hq, Hkv, S_max, group;
     int32_t chunk, nsplit;
     float c;  // scale * log2(e)
+    // paged cache: token t of sequence b is row t & (2^page_shift - 1) of page
+    // block_table[b * bt_s + (t >> page_shift)]; ks_b / vs_b are then the page strides
+    const int32_t* block_table;
+    int64_t bt_s;
+    int32_t page_shift, num_pages;
 };
 
 constexpr int kDecodeChunk = 128;
@@ -50,7 +55,9 @@ size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t 
 
 // G heads per workgroup, D head dim, TPW tokens per wave (chunk = 4 * TPW, sub-blocks of at most 64
 // tokens per wave; all trip counts are compile-time so each sub-block's loads issue together).
-template <typename T, int D, int G, int TPW>
+// PAGED: rows are addressed through the block table with 64-bit loads guarded by the length;
+// otherwise through a buffer resource over the chunk's rows.
+template <typename T, int D, int G, int TPW, bool PAGED>
 __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     constexpr int LPT = D / 8;            // lanes per token row
     constexpr int TPI = 64 / LPT;         // tokens per wave-wide load
@@ -95,10 +102,13 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
 
     const int kpitch = (int)(p.ks_s * (int64_t)sizeof(T));
     const int vpitch = (int)(p.vs_s * (int64_t)sizeof(T));
-    const T* kp = reinterpret_cast<const T*>(p.k) + b * p.ks_b + hk * p.ks_h + (int64_t)t0 * p.ks_s;
-    const T* vp = reinterpret_cast<const T*>(p.v) + b * p.vs_b + hk * p.vs_h + (int64_t)t0 * p.vs_s;
+    const int64_t kbo = PAGED ? 0 : b * p.ks_b + (int64_t)t0 * p.ks_s;
+    const int64_t vbo = PAGED ? 0 : b * p.vs_b + (int64_t)t0 * p.vs_s;
+    const T* kp = reinterpret_cast<const T*>(p.k) + hk * p.ks_h + kbo;
+    const T* vp = reinterpret_cast<const T*>(p.v) + hk * p.vs_h + vbo;
     const auto krs = make_rsrc(kp, (uint32_t)((n_tok - 1) * kpitch + D * (int)sizeof(T)));
     const auto vrs = make_rsrc(vp, (uint32_t)((n_tok - 1) * vpitch + D * (int)sizeof(T)));
+    const int32_t* bt = PAGED ? p.block_table + b * p.bt_s : nullptr;
 
     float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -112,11 +122,32 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb) {
         u32x4 kr[NI], vr[NI];
+        if constexpr (PAGED) {
+            int pg[NI];
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int tl = wave * TPW + sb * SB + i * TPI + tsub;
-            kr[i] = buf_ld16_nt(krs, (uint32_t)(tl * kpitch + c8 * 16));  // the cache is read once per call
-            vr[i] = buf_ld16_nt(vrs, (uint32_t)(tl * vpitch + c8 * 16));
+            for (int i = 0; i < NI; ++i) {
+                const int t = t0 + wave * TPW + sb * SB + i * TPI + tsub;
+                pg[i] = t < L ? min(max(bt[t >> p.page_shift], 0), p.num_pages - 1) : 0;
+            }
+            const int rmask = (1 << p.page_shift) - 1;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int t = t0 + wave * TPW + sb * SB + i * TPI + tsub;
+                u32x4 kz = {0u, 0u, 0u, 0u}, vz = {0u, 0u, 0u, 0u};
+                if (t < L) {  // the cache is read once per call
+                    kz = ld16_nt(kp + pg[i] * p.ks_b + (t & rmask) * p.ks_s + c8 * 8);
+                    vz = ld16_nt(vp + pg[i] * p.vs_b + (t & rmask) * p.vs_s + c8 * 8);
+                }
+                kr[i] = kz;
+                vr[i] = vz;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int tl = wave * TPW + sb * SB + i * TPI + tsub;
+                kr[i] = buf_ld16_nt(krs, (uint32_t)(tl * kpitch + c8 * 16));  // the cache is read once per call
+                vr[i] = buf_ld16_nt(vrs, (uint32_t)(tl * vpitch + c8 * 16));
+            }
         }
         float sc[NI][G];
 #pragma unroll
@@ -266,10 +297,10 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p)
     if (p.lse != nullptr && lane == 0) p.lse[b * p.lses_b + hq] = mx + __logf(sum);
 }
 
-template <typename T, int D, int G, int TPW>
+template <typename T, int D, int G, int TPW, bool PAGED>
 static int launch_decode(const DecodeParams& p, hipStream_t stream) {
     dim3 grid((unsigned)p.nsplit, (unsigned)(p.Hkv * (p.group / G)), (unsigned)p.B);
-    hipLaunchKernelGGL((decode_kernel<T, D, G, TPW>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_kernel<T, D, G, TPW, PAGED>), grid, dim3(256), 0, stream, p);
     int st = check_launch("decode_kernel");
     if (st != DTATTN_OK) return st;
     const int64_t pairs = (int64_t)p.B * p.Hq;
@@ -277,29 +308,29 @@ static int launch_decode(const DecodeParams& p, hipStream_t stream) {
     return check_launch("decode_merge_kernel");
 }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, bool PAGED>
 static int dispatch_chunk(const DecodeParams& p, hipStream_t stream) {
     switch (p.chunk) {
-        case 128: return launch_decode<T, D, G, 32>(p, stream);
-        case 256: return launch_decode<T, D, G, 64>(p, stream);
-        case 512: return launch_decode<T, D, G, 128>(p, stream);
+        case 128: return launch_decode<T, D, G, 32, PAGED>(p, stream);
+        case 256: return launch_decode<T, D, G, 64, PAGED>(p, stream);
+        case 512: return launch_decode<T, D, G, 128, PAGED>(p, stream);
         default: return fail(DTATTN_ERR_UNSUPPORTED, "decode: chunk %d not supported (128, 256, 512)", p.chunk);
     }
 }
 
-template <typename T, int D>
+template <typename T, int D, bool PAGED>
 static int dispatch_group(const DecodeParams& p, hipStream_t stream) {
     const int g = p.group;
-    if (g % 8 == 0) return dispatch_chunk<T, D, 8>(p, stream);
-    if (g % 4 == 0) return dispatch_chunk<T, D, 4>(p, stream);
-    if (g % 2 == 0) return dispatch_chunk<T, D, 2>(p, stream);
-    return dispatch_chunk<T, D, 1>(p, stream);
+    if (g % 8 == 0) return dispatch_chunk<T, D, 8, PAGED>(p, stream);
+    if (g % 4 == 0) return dispatch_chunk<T, D, 4, PAGED>(p, stream);
+    if (g % 2 == 0) return dispatch_chunk<T, D, 2, PAGED>(p, stream);
+    return dispatch_chunk<T, D, 1, PAGED>(p, stream);
 }
 
-template <typename T>
+template <typename T, bool PAGED>
 static int dispatch_decode(const DecodeParams& p, int D, hipStream_t stream) {
-    if (D == 128) return dispatch_group<T, 128>(p, stream);
-    if (D == 64) return dispatch_group<T, 64>(p, stream);
+    if (D == 128) return dispatch_group<T, 128, PAGED>(p, stream);
+    if (D == 64) return dispatch_group<T, 64, PAGED>(p, stream);
     return fail(DTATTN_ERR_UNSUPPORTED, "decode: head dim %d not supported (64 or 128)", D);
 }
 
@@ -364,11 +395,89 @@ extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_)
     p.Hkv = (int32_t)a->Hkv;
     p.S_max = (int32_t)a->S_max;
     p.group = (int32_t)(a->Hq / a->Hkv);
-    p.sub = 0;
     p.chunk = chunk;
     p.nsplit = (int32_t)nsplit;
     const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
     p.c = scale * kLog2e;
-    if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t>(p, (int)a->D, stream);
-    return dispatch_decode<f16_t>(p, (int)a->D, stream);
+    p.block_table = nullptr;
+    p.bt_s = 0;
+    p.page_shift = 0;
+    p.num_pages = 0;
+    if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, false>(p, (int)a->D, stream);
+    return dispatch_decode<f16_t, false>(p, (int)a->D, stream);
+}
+
+extern "C" size_t dtattn_decode_paged_workspace_size(int64_t B, int64_t Hq, int64_t max_pages, int64_t page_size,
+                                                     int64_t D, int32_t chunk) {
+    if (chunk <= 0) chunk = kDecodeChunk;
+    if (B <= 0 || Hq <= 0 || max_pages <= 0 || page_size <= 0 || D <= 0) return 0;
+    return decode_ws_parts(B, Hq, max_pages * page_size, D, chunk, nullptr);
+}
+
+extern "C" int dtattn_decode_paged(const dtattn_decode_paged_args* a, void* stream_) {
+    if (a == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: args is NULL");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (a->B < 0 || a->Hq <= 0 || a->Hkv <= 0 || a->D <= 0 || a->num_pages <= 0 || a->max_pages <= 0)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: bad sizes");
+    if (a->page_size < 16 || (a->page_size & (a->page_size - 1)) != 0 || a->page_size > (1 << 20))
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: page_size %lld must be a power of two >= 16",
+                    (long long)a->page_size);
+    if (a->Hq % a->Hkv != 0) return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: Hq is not a multiple of Hkv");
+    const int64_t S_max = a->max_pages * a->page_size;
+    if (S_max > (1 << 29) || a->num_pages > 0x7fffffff)
+        return fail(DTATTN_ERR_UNSUPPORTED, "decode_paged: cache too large");
+    if (a->B == 0) return DTATTN_OK;
+    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16)
+        return fail(DTATTN_ERR_UNSUPPORTED, "decode_paged: dtype %d not supported (bf16, fp16)", a->dtype);
+    const int32_t chunk = a->chunk > 0 ? a->chunk : kDecodeChunk;
+    if (chunk != 128 && chunk != 256 && chunk != 512)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: chunk %d must be 128, 256 or 512", chunk);
+    if (a->q == nullptr || a->k_pages == nullptr || a->v_pages == nullptr || a->block_table == nullptr ||
+        a->lengths == nullptr || a->o == nullptr)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: null pointer");
+    const int64_t esz = 2;
+    const int64_t s_all[] = {a->q_stride[0], a->q_stride[1], a->k_stride[0], a->k_stride[1], a->k_stride[2],
+                             a->v_stride[0], a->v_stride[1], a->v_stride[2]};
+    for (int64_t s : s_all)
+        if ((s * esz) % 16 != 0)
+            return fail(DTATTN_ERR_UNSUPPORTED, "decode_paged: strides must be multiples of 16 bytes");
+    int64_t nsplit = 0;
+    const size_t need = decode_ws_parts(a->B, a->Hq, S_max, a->D, chunk, &nsplit);
+    if (a->workspace == nullptr || a->workspace_bytes < need)
+        return fail(DTATTN_ERR_WORKSPACE, "decode_paged: workspace of %zu bytes required, %zu given", need,
+                    a->workspace_bytes);
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
+        return fail(DTATTN_ERR_WORKSPACE, "decode_paged: workspace must be 256-byte aligned");
+    if (nsplit > 65535 || a->B > 65535) return fail(DTATTN_ERR_UNSUPPORTED, "decode_paged: grid too large");
+
+    DecodeParams p;
+    p.q = a->q;
+    p.k = a->k_pages;
+    p.v = a->v_pages;
+    p.lengths = a->lengths;
+    p.o = a->o;
+    p.lse = a->lse;
+    const size_t o_bytes = (size_t)a->B * a->Hq * nsplit * a->D * sizeof(float);
+    p.part_o = reinterpret_cast<float*>(a->workspace);
+    p.part_lse = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + ((o_bytes + 255) & ~(size_t)255));
+    p.qs_b = a->q_stride[0], p.qs_h = a->q_stride[1];
+    p.ks_b = a->k_stride[0], p.ks_h = a->k_stride[1], p.ks_s = a->k_stride[2];  // page, H, row
+    p.vs_b = a->v_stride[0], p.vs_h = a->v_stride[1], p.vs_s = a->v_stride[2];
+    p.os_b = a->o_stride[0], p.os_h = a->o_stride[1];
+    p.lses_b = a->lse ? a->lse_stride[0] : 0;
+    p.B = (int32_t)a->B;
+    p.Hq = (int32_t)a->Hq;
+    p.Hkv = (int32_t)a->Hkv;
+    p.S_max = (int32_t)S_max;
+    p.group = (int32_t)(a->Hq / a->Hkv);
+    p.chunk = chunk;
+    p.nsplit = (int32_t)nsplit;
+    const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
+    p.c = scale * kLog2e;
+    p.block_table = a->block_table;
+    p.bt_s = a->block_table_stride;
+    p.page_shift = __builtin_ctzll((unsigned long long)a->page_size);
+    p.num_pages = (int32_t)a->num_pages;
+    if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, true>(p, (int)a->D, stream);
+    return dispatch_decode<f16_t, true>(p, (int)a->D, stream);
 }

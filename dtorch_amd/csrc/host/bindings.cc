@@ -80,6 +80,12 @@ PYBIND11_MODULE(_dtattn_host, m) {
             return RunCompute([&](const TorchTensorOptArray& i, TorchTensorArray& o) { op.Compute(i, o); }, in);
         });
 
+    py::class_<SdpaDecodePagedOp>(m, "SdpaDecodePagedOp")
+        .def(py::init<std::optional<double>, int32_t>(), py::arg("scale") = std::nullopt, py::arg("chunk") = 0)
+        .def("compute", [](const SdpaDecodePagedOp& op, const std::vector<std::optional<at::Tensor>>& in) {
+            return RunCompute([&](const TorchTensorOptArray& i, TorchTensorArray& o) { op.Compute(i, o); }, in);
+        });
+
     py::class_<LseMergeOp>(m, "LseMergeOp")
         .def(py::init<std::optional<c10::ScalarType>>(), py::arg("out_dtype") = std::nullopt)
         .def("compute", [](const LseMergeOp& op, const std::vector<std::optional<at::Tensor>>& in) {

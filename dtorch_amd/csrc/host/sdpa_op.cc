@@ -323,6 +323,63 @@ void SdpaDecodeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& 
     outputs.push_back(lse);
 }
 
+void SdpaDecodePagedOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
+    if (inputs.size() != 5 || !inputs[0] || !inputs[1] || !inputs[2] || !inputs[3] || !inputs[4])
+        Throw("SdpaDecodePagedOp expects 5 inputs {query, k_pages, v_pages, block_table, lengths}");
+    const at::Tensor &q = *inputs[0], &kp = *inputs[1], &vp = *inputs[2], &bt = *inputs[3], &len = *inputs[4];
+    CheckDevice({&q, &kp, &vp, &bt, &len});
+    c10::DeviceGuard guard(q.device());
+    if (q.dim() != 4 || kp.dim() != 4 || vp.dim() != 4) Throw("query and page pools must be 4-D");
+    if (q.size(2) != 1) Throw("decode query must have one token per sequence ([B, Hq, 1, D])");
+    if (kp.sizes() != vp.sizes()) Throw("k_pages and v_pages shapes differ");
+    if (q.size(3) != kp.size(3)) Throw("query and page head dims differ");
+    if (kp.size(1) <= 0 || q.size(1) % kp.size(1) != 0) Throw("number of query heads must be a multiple of kv heads");
+    if (bt.scalar_type() != at::kInt || bt.dim() != 2 || bt.size(0) != q.size(0))
+        Throw("block_table must be an int32 tensor of shape [B, max_pages]");
+    if (len.scalar_type() != at::kInt || len.dim() != 1 || len.size(0) != q.size(0))
+        Throw("lengths must be an int32 tensor of shape [B]");
+    const c10::ScalarType st = q.scalar_type();
+    if (kp.scalar_type() != st || vp.scalar_type() != st) Throw("query and page dtypes differ");
+    if (st != at::kBFloat16 && st != at::kHalf) Throw("decode supports bf16 and fp16");
+    if (mScale.has_value() && !(mScale.value() > 0.0)) Throw("scale must be positive");
+    if (kp.stride(3) != 1 || vp.stride(3) != 1) Throw("page pools need a unit stride along D");
+
+    at::Tensor o = at::empty(q.sizes(), q.options());
+    at::Tensor lse = at::empty({q.size(0), q.size(1)}, q.options().dtype(at::kFloat));
+    if (q.size(0) == 0) {
+        outputs.push_back(o);
+        outputs.push_back(lse);
+        return;
+    }
+    View4 qv = MakeView4(q, "query");
+    at::Tensor btc = bt.stride(1) == 1 ? bt : bt.contiguous();
+    at::Tensor lc = len.contiguous();
+    dtattn_decode_paged_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = qv.t.data_ptr(), a.k_pages = kp.data_ptr(), a.v_pages = vp.data_ptr();
+    a.block_table = btc.data_ptr<int32_t>();
+    a.lengths = lc.data_ptr<int32_t>();
+    a.o = o.data_ptr(), a.lse = lse.data_ptr<float>();
+    a.B = qv.B, a.Hq = qv.H, a.Hkv = kp.size(1), a.D = qv.D;
+    a.num_pages = kp.size(0), a.page_size = kp.size(2), a.max_pages = bt.size(1);
+    a.q_stride[0] = qv.sb, a.q_stride[1] = qv.sh;
+    a.k_stride[0] = kp.stride(0), a.k_stride[1] = kp.stride(1), a.k_stride[2] = kp.stride(2);
+    a.v_stride[0] = vp.stride(0), a.v_stride[1] = vp.stride(1), a.v_stride[2] = vp.stride(2);
+    a.o_stride[0] = q.size(1) * q.size(3), a.o_stride[1] = q.size(3);
+    a.lse_stride[0] = q.size(1);
+    a.block_table_stride = btc.stride(0);
+    a.dtype = DtypeCode(st);
+    a.scale = mScale.has_value() ? (float)mScale.value() : 0.f;
+    a.chunk = mChunk;
+    const size_t ws = dtattn_decode_paged_workspace_size(a.B, a.Hq, a.max_pages, a.page_size, a.D, a.chunk);
+    at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, q.options().dtype(at::kByte));
+    a.workspace = wst.data_ptr();
+    a.workspace_bytes = ws;
+    Check(dtattn_decode_paged(&a, CurrentStream(q)), "dtattn_decode_paged");
+    outputs.push_back(o);
+    outputs.push_back(lse);
+}
+
 void LseMergeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
     if (inputs.empty() || inputs.size() % 2 != 0) Throw("LseMergeOp expects pairs {O_0, LSE_0, O_1, LSE_1, ...}");
     const int n = (int)inputs.size() / 2;

@@ -10,6 +10,7 @@
 // New operators (no reference counterpart; registered the same way an operator is added to DTorch):
 //   SdpaWithLseOp  -> {O, LSE}, with explicit causal offsets for ring blocks
 //   SdpaDecodeOp   -> {O, LSE} for one query token per sequence against a padded KV cache
+//   SdpaDecodePagedOp -> the same against a paged KV cache (page pool + block table)
 //   LseMergeOp     -> {O, LSE} from n (O_b, LSE_b) pairs
 //   Fp8QuantizeOp  -> {codes, descale}, per-head absmax e4m3fn
 #pragma once
@@ -103,6 +104,19 @@ private:
 class SdpaDecodeOp {
 public:
     SdpaDecodeOp(std::optional<double> scale, int32_t chunk) : mScale(scale), mChunk(chunk) {}
+    void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
+
+private:
+    std::optional<double> mScale;
+    int32_t mChunk;
+};
+
+// {q[B,Hq,1,D], k_pages[P,Hkv,page,D], v_pages[P,Hkv,page,D], block_table[B,max_pages] int32,
+//  lengths[B] int32} -> {O[B,Hq,1,D], LSE[B,Hq]}.  The page pools may be any 4-D view whose axes are
+// (page, kv head, row within the page, D) with a unit D stride (e.g. a permuted [P,page,Hkv,D] pool).
+class SdpaDecodePagedOp {
+public:
+    SdpaDecodePagedOp(std::optional<double> scale, int32_t chunk) : mScale(scale), mChunk(chunk) {}
     void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
 
 private:

@@ -116,6 +116,22 @@ def decode_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
     return o, lse
 
 
+def decode_attention_paged(query: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                           block_table: torch.Tensor, lengths: torch.Tensor, scale: Optional[float] = None,
+                           chunk: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """decode_attention over a paged KV cache.
+
+    query [B, Hq, 1, D]; k_pages / v_pages are page pools viewed as [num_pages, Hkv, page_size, D]
+    (any strides with unit stride on D, so a [num_pages, page_size, Hkv, D] pool passed through
+    .permute(0, 2, 1, 3) works without a copy); block_table int32 [B, max_pages] holds the page of
+    each sequence's p-th block; lengths int32 [B].  page_size is a power of two >= 16.
+    Returns (O [B, Hq, 1, D], LSE [B, Hq] fp32).
+    """
+    op = _h.SdpaDecodePagedOp(None if scale is None else float(scale), int(chunk))
+    o, lse = op.compute([query, k_pages, v_pages, block_table, lengths])
+    return o, lse
+
+
 def lse_merge(outs: Sequence[torch.Tensor], lses: Sequence[torch.Tensor],
               out_dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Merge partial attention blocks over the same queries by their LSE."""

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define DTATTN_ABI_VERSION 1
+#define DTATTN_ABI_VERSION 2
 
 typedef enum {
     DTATTN_OK = 0,
@@ -107,6 +107,41 @@ typedef struct {
 
 size_t dtattn_decode_workspace_size(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk);
 int dtattn_decode_splitkv(const dtattn_decode_args* args, void* stream);
+
+/* Split-KV single-token decode against a paged KV cache.
+ *
+ * No counterpart in the reference (the next step its survey lists for decode: a KV cache feeding the
+ * decode operator, python/dtorch/test/modules/llama.py:126-156).  Same arithmetic as
+ * dtattn_decode_splitkv; token t of sequence b lives in page block_table[b][t / page_size] at row
+ * t % page_size.  Page ids are clamped to [0, num_pages), so a corrupt block table reads wrong rows
+ * but never leaves the pool; rows at or past lengths[b] are never read.
+ */
+typedef struct {
+    const void* q;             /* [B, Hq, 1, D] */
+    const void* k_pages;       /* page pool, e.g. [num_pages, Hkv, page_size, D] (any strides below) */
+    const void* v_pages;
+    const int32_t* block_table;/* [B, max_pages] device int32 */
+    const int32_t* lengths;    /* [B] device int32; clamped to [0, max_pages * page_size] */
+    void* o;                   /* [B, Hq, 1, D], same dtype as q */
+    float* lse;                /* [B, Hq] fp32; may be NULL */
+    int64_t B, Hq, Hkv, D;
+    int64_t num_pages, page_size, max_pages;  /* page_size: a power of two >= 16 */
+    int64_t q_stride[2];       /* B, H */
+    int64_t k_stride[3];       /* page, H, row within the page */
+    int64_t v_stride[3];
+    int64_t o_stride[2];       /* B, H */
+    int64_t lse_stride[1];     /* B (H stride is 1) */
+    int64_t block_table_stride;/* elements between rows of block_table */
+    int32_t dtype;             /* BF16 or FP16 */
+    float scale;               /* <= 0 means 1/sqrt(D) */
+    int32_t chunk;             /* tokens per split: 128, 256 or 512; 0 picks the default (128) */
+    void* workspace;           /* >= dtattn_decode_paged_workspace_size(...) bytes, 256-byte aligned */
+    size_t workspace_bytes;
+} dtattn_decode_paged_args;
+
+size_t dtattn_decode_paged_workspace_size(int64_t B, int64_t Hq, int64_t max_pages, int64_t page_size, int64_t D,
+                                          int32_t chunk);
+int dtattn_decode_paged(const dtattn_decode_paged_args* args, void* stream);
 
 /* LSE merge of n partial attention blocks over the same queries.
  *

@@ -132,6 +132,29 @@ def decode(q, k_cache, v_cache, lengths, scale: Optional[float] = None) -> Tuple
     return np.stack(outs), np.stack(lses)
 
 
+def gather_pages(pages, block_table, lengths, max_len: Optional[int] = None) -> np.ndarray:
+    """Contiguous [B, Hkv, S, D] cache rebuilt from a paged one: token t of sequence b is row
+    t % page_size of page block_table[b, t // page_size] in pages [num_pages, Hkv, page_size, D].
+    Rows at or past lengths[b] are left zero and never looked up."""
+    pages = np.asarray(pages)
+    _, hkv, ps, d = pages.shape
+    B = len(lengths)
+    S = int(max_len if max_len is not None else max(int(x) for x in lengths))
+    out = np.zeros((B, hkv, S, d), dtype=pages.dtype)
+    for b in range(B):
+        for t in range(int(lengths[b])):
+            out[b, :, t] = pages[int(block_table[b][t // ps]), :, t % ps]
+    return out
+
+
+def decode_paged(q, k_pages, v_pages, block_table, lengths, scale: Optional[float] = None):
+    """Single-token decode over a paged KV cache: ``decode`` on the cache that ``gather_pages``
+    rebuilds (new path, no reference function)."""
+    kc = gather_pages(k_pages, block_table, lengths)
+    vc = gather_pages(v_pages, block_table, lengths)
+    return decode(q, kc, vc, lengths, scale=scale)
+
+
 def lse_merge(os: Sequence[np.ndarray], lses: Sequence[np.ndarray]) -> Tuple[np.ndarray, np.ndarray]:
     """Merge partial attention blocks by their log-sum-exp (closed form, no reference function).
 

@@ -210,3 +210,139 @@ def test_decode_zero_length_sequences():
     ro, rl = orc.decode(rounded(q[[1, 3]]), rounded(kc[[1, 3]]), rounded(vc[[1, 3]]), lengths[[1, 3]])
     assert max_abs(o[[1, 3]], ro) <= O_TOL_BF16
     assert lse_rel(lse[[1, 3]], rl[..., 0]) <= LSE_TOL
+
+
+# --------------------------------------------------------------------------- paged decode
+
+def _paged_pool(rng, lengths, Hkv, D, ps, spare_pages=3, token_major=False, dtype=torch.bfloat16):
+    """A page pool holding each sequence's tokens on randomly chosen pages, NaN on the pages no
+    sequence uses, and a block table whose unused slots hold an id far outside the pool."""
+    need = [(int(L) + ps - 1) // ps for L in lengths]
+    P = sum(need) + spare_pages
+    max_pages = max(max(need), 1) + 1
+    perm = rng.permutation(P)
+    bt = np.full((len(lengths), max_pages), 1 << 30, dtype=np.int32)
+    used, off = set(), 0
+    for b, n in enumerate(need):
+        bt[b, :n] = perm[off:off + n]
+        used.update(int(x) for x in perm[off:off + n])
+        off += n
+    kp = randn(rng, (P, Hkv, ps, D))
+    vp = randn(rng, (P, Hkv, ps, D))
+    free = [p for p in range(P) if p not in used]
+    kp[free] = np.nan
+    vp[free] = np.nan
+    # rows past the end of the last page of each sequence are never read either
+    for b, L in enumerate(lengths):
+        if int(L) % ps:
+            last = bt[b, need[b] - 1]
+            kp[last, :, int(L) % ps:] = np.nan
+            vp[last, :, int(L) % ps:] = np.nan
+    if token_major:  # pool stored [P, ps, Hkv, D], handed over as a permuted view
+        tk = to_dev(kp.transpose(0, 2, 1, 3), dtype).permute(0, 2, 1, 3)
+        tv = to_dev(vp.transpose(0, 2, 1, 3), dtype).permute(0, 2, 1, 3)
+    else:
+        tk, tv = to_dev(kp, dtype), to_dev(vp, dtype)
+    return kp, vp, tk, tv, bt, max_pages
+
+
+def _gather_dev(pool, bt, lengths, S):
+    """Contiguous [B, Hkv, S, D] device cache with the paged cache's tokens, zeros elsewhere."""
+    B = len(lengths)
+    out = torch.zeros((B, pool.shape[1], S, pool.shape[3]), dtype=pool.dtype, device=pool.device)
+    ps = pool.shape[2]
+    for b in range(B):
+        L = int(lengths[b])
+        if L == 0:
+            continue
+        t = torch.arange(L, device=pool.device)
+        pages = torch.from_numpy(bt[b]).to(pool.device).long()[t // ps]
+        out[b, :, :L] = pool[pages, :, t % ps].permute(1, 0, 2)
+    return out
+
+
+@pytest.mark.parametrize("ps,B,Hq,Hkv,D,lengths,chunk,token_major", [
+    (16, 3, 32, 8, 128, [1, 250, 513], 0, False),
+    (64, 4, 8, 8, 128, [64, 65, 300, 0], 0, False),      # MHA, page-aligned and empty sequences
+    (128, 2, 16, 2, 128, [700, 129], 256, True),         # GQA 8, token-major pool
+    (256, 2, 12, 2, 128, [1000, 77], 512, False),        # GQA 6
+    (16, 2, 8, 4, 64, [519, 3], 128, True),              # D = 64
+])
+def test_decode_paged_small(ps, B, Hq, Hkv, D, lengths, chunk, token_major):
+    rng = np.random.default_rng(ps + B)
+    q = randn(rng, (B, Hq, 1, D))
+    lengths = np.asarray(lengths, dtype=np.int32)
+    kp, vp, tk, tv, bt, max_pages = _paged_pool(rng, lengths, Hkv, D, ps, token_major=token_major)
+    F = _F()
+    tq, tl = to_dev(q), torch.from_numpy(lengths).cuda()
+    o, lse = F.decode_attention_paged(tq, tk, tv, torch.from_numpy(bt).cuda(), tl, chunk=chunk)
+    torch.cuda.synchronize()
+    ho, hl = host(o), host(lse)
+    for b in np.flatnonzero(lengths == 0):
+        assert np.all(ho[b] == 0) and np.all(np.isneginf(hl[b])), b
+    nz = np.flatnonzero(lengths > 0)
+    ro, rl = orc.decode_paged(rounded(q[nz]), rounded(np.nan_to_num(kp)), rounded(np.nan_to_num(vp)),
+                              bt[nz], lengths[nz])
+    assert max_abs(ho[nz], ro) <= O_TOL_BF16
+    assert lse_rel(hl[nz], rl[..., 0]) <= LSE_TOL
+    # same arithmetic as the contiguous decode over the gathered cache of S_max = max_pages * page_size
+    S = max_pages * ps
+    co, cl = F.decode_attention(tq, _gather_dev(tk, bt, lengths, S), _gather_dev(tv, bt, lengths, S), tl,
+                                chunk=chunk)
+    torch.cuda.synchronize()
+    assert torch.equal(o, co)
+    assert torch.equal(lse, cl)
+
+
+def test_decode_paged_fp16_and_errors():
+    rng = np.random.default_rng(21)
+    lengths = np.array([333, 40], dtype=np.int32)
+    q = randn(rng, (2, 8, 1, 128))
+    kp, vp, tk, tv, bt, _ = _paged_pool(rng, lengths, 2, 128, 32, dtype=torch.float16)
+    F = _F()
+    tb, tl = torch.from_numpy(bt).cuda(), torch.from_numpy(lengths).cuda()
+    o, lse = F.decode_attention_paged(to_dev(q, torch.float16), tk, tv, tb, tl)
+    torch.cuda.synchronize()
+    ro, rl = orc.decode_paged(rounded(q, torch.float16), rounded(np.nan_to_num(kp), torch.float16),
+                              rounded(np.nan_to_num(vp), torch.float16), bt, lengths)
+    assert max_abs(host(o), ro) <= O_TOL_BF16
+    assert lse_rel(host(lse), rl[..., 0]) <= LSE_TOL
+    with pytest.raises(ValueError, match="page"):  # page size 24 is not a power of two
+        F.decode_attention_paged(to_dev(q, torch.float16), tk[:, :, :24], tv[:, :, :24], tb, tl)
+    with pytest.raises(ValueError):
+        F.decode_attention_paged(to_dev(q, torch.float16), tk, tv, tb.long(), tl)
+
+
+def test_config3_decode_paged_full_size():
+    # the full-size decode workload (B=64, Hq=32, Hkv=8, D=128, lengths ~ U[512, 8192]) in 16-token
+    # pages scattered over the pool: bit-identical to the contiguous decode over the gathered cache,
+    # and sampled sequences against the oracle
+    rng = np.random.default_rng(5)
+    B, Hq, Hkv, D, ps = 64, 32, 8, 128, 16
+    lengths = rng.integers(512, 8192, size=B, endpoint=True).astype(np.int32)
+    need = (lengths + ps - 1) // ps
+    P = int(need.sum())
+    max_pages = int(need.max())
+    perm = rng.permutation(P).astype(np.int32)
+    bt = np.zeros((B, max_pages), dtype=np.int32)
+    off = 0
+    for b in range(B):
+        bt[b, :need[b]] = perm[off:off + need[b]]
+        off += need[b]
+    g = torch.Generator(device="cuda").manual_seed(5)
+    tk = torch.randn((P, Hkv, ps, D), generator=g, device="cuda").to(torch.bfloat16)
+    tv = torch.randn((P, Hkv, ps, D), generator=g, device="cuda").to(torch.bfloat16)
+    tq = torch.randn((B, Hq, 1, D), generator=g, device="cuda").to(torch.bfloat16)
+    tb, tl = torch.from_numpy(bt).cuda(), torch.from_numpy(lengths).cuda()
+    F = _F()
+    o, lse = F.decode_attention_paged(tq, tk, tv, tb, tl)
+    S = max_pages * ps
+    kc, vc = _gather_dev(tk, bt, lengths, S), _gather_dev(tv, bt, lengths, S)
+    co, cl = F.decode_attention(tq, kc, vc, tl)
+    torch.cuda.synchronize()
+    assert torch.equal(o, co)
+    assert torch.equal(lse, cl)
+    pick = [0, int(np.argmax(lengths)), int(np.argmin(lengths)), B - 1]
+    ro, rl = orc.decode(host(tq[pick]), host(kc[pick]), host(vc[pick]), lengths[pick])
+    assert max_abs(host(o[pick]), ro) <= O_TOL_BF16
+    assert lse_rel(host(lse[pick]), rl[..., 0]) <= LSE_TOL

@@ -119,6 +119,36 @@ def test_workspace_sizes():
     assert lib.dtattn_fp8_quantize_workspace_size(1, 24, 4608, 128) == ((24 * 18 * 4 + 255) // 256) * 256
 
 
+def test_decode_paged_validation():
+    class PagedArgs(ctypes.Structure):
+        _fields_ = [("q", ctypes.c_void_p), ("k_pages", ctypes.c_void_p), ("v_pages", ctypes.c_void_p),
+                    ("block_table", ctypes.c_void_p), ("lengths", ctypes.c_void_p), ("o", ctypes.c_void_p),
+                    ("lse", ctypes.c_void_p), ("B", ctypes.c_int64), ("Hq", ctypes.c_int64),
+                    ("Hkv", ctypes.c_int64), ("D", ctypes.c_int64), ("num_pages", ctypes.c_int64),
+                    ("page_size", ctypes.c_int64), ("max_pages", ctypes.c_int64), ("q_stride", ctypes.c_int64 * 2),
+                    ("k_stride", ctypes.c_int64 * 3), ("v_stride", ctypes.c_int64 * 3),
+                    ("o_stride", ctypes.c_int64 * 2), ("lse_stride", ctypes.c_int64 * 1),
+                    ("block_table_stride", ctypes.c_int64), ("dtype", ctypes.c_int32), ("scale", ctypes.c_float),
+                    ("chunk", ctypes.c_int32), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
+    lib.dtattn_decode_paged.restype = ctypes.c_int
+    a = PagedArgs()
+    a.B, a.Hq, a.Hkv, a.D, a.num_pages, a.max_pages = 2, 8, 2, 128, 10, 4
+    a.page_size = 48  # not a power of two
+    assert lib.dtattn_decode_paged(ctypes.byref(a), None) == 1 and "page_size" in _last_error()
+    a.page_size = 16
+    a.Hq = 5  # not a multiple of Hkv
+    assert lib.dtattn_decode_paged(ctypes.byref(a), None) == 1 and "multiple" in _last_error()
+    a.Hq = 8
+    assert lib.dtattn_decode_paged(ctypes.byref(a), None) == 1 and "null" in _last_error()
+    lib.dtattn_decode_paged_workspace_size.restype = ctypes.c_size_t
+    lib.dtattn_decode_paged_workspace_size.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int32]
+    lib.dtattn_decode_workspace_size.restype = ctypes.c_size_t
+    lib.dtattn_decode_workspace_size.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_int32]
+    # the paged workspace is the padded one for S_max = max_pages * page_size
+    assert lib.dtattn_decode_paged_workspace_size(64, 32, 512, 16, 128, 0) == \
+        lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 0)
+
+
 def test_merge_validation():
     class MergeArgs(ctypes.Structure):
         _fields_ = [("n_blocks", ctypes.c_int32), ("o_blocks", ctypes.c_void_p * 16),

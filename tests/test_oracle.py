@@ -157,6 +157,36 @@ def test_decode_equals_prefill_at_lq1():
     assert not np.allclose(o3, o[1])
 
 
+def test_paged_cache_round_trip_and_decode():
+    # Scatter a contiguous cache into a shuffled page pool with an independent fancy-indexing write,
+    # then gather_pages must rebuild it bit for bit and decode_paged must equal decode; the pool's
+    # unused pages hold NaN, so reading a wrong page or a row past the length would show.
+    rng = np.random.default_rng(12)
+    B, Hq, Hkv, D, ps, max_pages = 3, 8, 2, 32, 16, 5
+    lengths = np.array([80, 1, 37])
+    q = rng.standard_normal((B, Hq, 1, D))
+    kc, vc = (rng.standard_normal((B, Hkv, max_pages * ps, D)) for _ in range(2))
+    num_pages = B * max_pages + 4
+    perm = rng.permutation(num_pages)[:B * max_pages].reshape(B, max_pages)
+    kp = np.full((num_pages, Hkv, ps, D), np.nan)
+    vp = np.full((num_pages, Hkv, ps, D), np.nan)
+    for b in range(B):
+        used = -(-int(lengths[b]) // ps)  # pages holding a token of sequence b
+        blocks = kc[b, :, :max_pages * ps].reshape(Hkv, max_pages, ps, D).transpose(1, 0, 2, 3)
+        vblocks = vc[b, :, :max_pages * ps].reshape(Hkv, max_pages, ps, D).transpose(1, 0, 2, 3)
+        kp[perm[b, :used]] = blocks[:used]
+        vp[perm[b, :used]] = vblocks[:used]
+    g = orc.gather_pages(kp, perm, lengths, max_len=max_pages * ps)
+    for b in range(B):
+        L = int(lengths[b])
+        assert np.array_equal(g[b, :, :L], kc[b, :, :L])
+        assert np.all(g[b, :, L:] == 0)
+    o, lse = orc.decode_paged(q, kp, vp, perm, lengths)
+    o2, l2 = orc.decode(q, kc, vc, lengths)
+    assert np.array_equal(o, o2) and np.array_equal(lse, l2)
+    assert np.all(np.isfinite(o))
+
+
 # --------------------------------------------------------------------------- merge
 
 def test_merge_equals_single_pass():
