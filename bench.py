@@ -134,7 +134,28 @@ def secondary_workloads(torch, F, dev, timer):
                            "note": "L2/MALL flushed before every rep"}
     log(f"decode B=64 Hq=32 Hkv=8 lengths U[512,8192]: {med * 1e6:.1f} us, {gbs:.0f} GB/s "
         f"({100 * gbs * 1e9 / PEAK_HBM:.1f}% of HBM)")
-    del kc, vc, qd
+
+    # the same caches in 16-token pages [P, Hkv, 16, D], scattered over the pool by a random block table
+    ps = 16
+    npg = Smax // ps
+    perm = torch.from_numpy(np.random.default_rng(1).permutation(Bd * npg).astype(np.int64)).to(dev)
+
+    def paged(c):
+        pool = torch.empty((Bd * npg, Hkvd, ps, Dd), dtype=c.dtype, device=dev)
+        pool[perm] = c.view(Bd, Hkvd, npg, ps, Dd).permute(0, 2, 1, 3, 4).reshape(Bd * npg, Hkvd, ps, Dd)
+        return pool
+
+    kp, vp = paged(kc), paged(vc)
+    del kc, vc
+    bt = perm.view(Bd, npg).to(torch.int32)
+    med_p, _ = timer.run(lambda: F.decode_attention_paged(qd, kp, vp, bt, lens), reps=20, flush=flush)
+    gbs_p = dbytes / med_p / 1e9
+    extras["decode_c3_paged16"] = {"GB/s": round(gbs_p, 1), "frac_hbm": round(gbs_p * 1e9 / PEAK_HBM, 4),
+                                   "us": round(med_p * 1e6, 1), "bytes": dbytes,
+                                   "note": "16-token pages in random pool order; L2/MALL flushed before every rep"}
+    log(f"paged decode, 16-token pages: {med_p * 1e6:.1f} us, {gbs_p:.0f} GB/s "
+        f"({100 * gbs_p * 1e9 / PEAK_HBM:.1f}% of HBM)")
+    del kp, vp, qd, bt, perm
 
     # ring step: 4 blocks (1 causal diagonal + 3 full) + merge
     C = 4096

@@ -31,7 +31,8 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     names = declared_functions()
-    for n in ["dtattn_prefill_fwd", "dtattn_decode_splitkv", "dtattn_decode_workspace_size", "dtattn_lse_merge",
+    for n in ["dtattn_prefill_fwd", "dtattn_decode_splitkv", "dtattn_decode_workspace_size", "dtattn_decode_paged",
+              "dtattn_decode_paged_workspace_size", "dtattn_lse_merge",
               "dtattn_fp8_quantize_per_head", "dtattn_fp8_quantize_workspace_size", "dtattn_get_device_peaks",
               "dtattn_last_error", "dtattn_abi_version"]:
         assert n in names
