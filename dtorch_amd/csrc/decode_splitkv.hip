@@ -55,7 +55,7 @@ size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t 
 
 // G heads per workgroup, D head dim, TPW tokens per wave (chunk = 4 * TPW, sub-blocks of at most 64
 // tokens per wave; all trip counts are compile-time so each sub-block's loads issue together).
-// PAGED: rows are addressed through the block table with 64-bit loads guarded by the length;
+// PAGED: rows are addressed through the block table with 64-bit loads of clamped token indices;
 // otherwise through a buffer resource over the chunk's rows.
 template <typename T, int D, int G, int TPW, bool PAGED>
 __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
@@ -123,23 +123,21 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     for (int sb = 0; sb < NSB; ++sb) {
         u32x4 kr[NI], vr[NI];
         if constexpr (PAGED) {
-            int pg[NI];
+            // Token indices past the sequence end are clamped to its last token (L >= 1 here), so every
+            // block-table and cache load is unconditional and a sub-block's loads issue together; those
+            // rows get score -inf below and P = 0.  Rows at or past lengths[b] are never read.
+            int pg[NI], tr[NI];
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
-                const int t = t0 + wave * TPW + sb * SB + i * TPI + tsub;
-                pg[i] = t < L ? min(max(bt[t >> p.page_shift], 0), p.num_pages - 1) : 0;
+                tr[i] = min(t0 + wave * TPW + sb * SB + i * TPI + tsub, L - 1);
+                pg[i] = min(max(bt[tr[i] >> p.page_shift], 0), p.num_pages - 1);
             }
+            __builtin_amdgcn_sched_barrier(0);
             const int rmask = (1 << p.page_shift) - 1;
 #pragma unroll
-            for (int i = 0; i < NI; ++i) {
-                const int t = t0 + wave * TPW + sb * SB + i * TPI + tsub;
-                u32x4 kz = {0u, 0u, 0u, 0u}, vz = {0u, 0u, 0u, 0u};
-                if (t < L) {  // the cache is read once per call
-                    kz = ld16_nt(kp + pg[i] * p.ks_b + (t & rmask) * p.ks_s + c8 * 8);
-                    vz = ld16_nt(vp + pg[i] * p.vs_b + (t & rmask) * p.vs_s + c8 * 8);
-                }
-                kr[i] = kz;
-                vr[i] = vz;
+            for (int i = 0; i < NI; ++i) {  // the cache is read once per call
+                kr[i] = ld16_nt(kp + pg[i] * p.ks_b + (tr[i] & rmask) * p.ks_s + c8 * 8);
+                vr[i] = ld16_nt(vp + pg[i] * p.vs_b + (tr[i] & rmask) * p.vs_s + c8 * 8);
             }
         } else {
 #pragma unroll
@@ -149,6 +147,10 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
                 vr[i] = buf_ld16_nt(vrs, (uint32_t)(tl * vpitch + c8 * 16));
             }
         }
+        // Every K and V load of the sub-block is in flight before the first use: left alone, the
+        // scheduler issues the V loads only after the QK products, which costs a second memory
+        // round trip per workgroup (measured: 4.42 -> 4.67 TB/s on the random-length batch).
+        __builtin_amdgcn_sched_barrier(0);
         float sc[NI][G];
 #pragma unroll
         for (int i = 0; i < NI; ++i) {

@@ -22,23 +22,29 @@ struct MergeParams {
     int32_t H, S, n;
 };
 
-// Block outputs are read exactly once: non-temporal loads.
+// Block outputs are read exactly once: non-temporal loads.  A chunk is the raw bits of 8 elements,
+// loaded before any of them is used so that a thread's loads are in flight together.
 template <typename TI>
-__device__ __forceinline__ void load8(const TI* p, float* out);
-template <>
-__device__ __forceinline__ void load8<bf16_t>(const bf16_t* p, float* out) {
-    unpack8<bf16_t>(ld16_nt(p), out);
+struct Chunk {
+    u32x4 v[sizeof(TI) == 4 ? 2 : 1];
+};
+template <typename TI>
+__device__ __forceinline__ Chunk<TI> load_chunk(const TI* p) {
+    Chunk<TI> c;
+    c.v[0] = ld16_nt(p);
+    if constexpr (sizeof(TI) == 4) c.v[1] = ld16_nt(p + 4);
+    return c;
 }
-template <>
-__device__ __forceinline__ void load8<f16_t>(const f16_t* p, float* out) {
-    unpack8<f16_t>(ld16_nt(p), out);
-}
-template <>
-__device__ __forceinline__ void load8<float>(const float* p, float* out) {
-    const f32x4 a = __builtin_bit_cast(f32x4, ld16_nt(p));
-    const f32x4 b = __builtin_bit_cast(f32x4, ld16_nt(p + 4));
-    out[0] = a.x, out[1] = a.y, out[2] = a.z, out[3] = a.w;
-    out[4] = b.x, out[5] = b.y, out[6] = b.z, out[7] = b.w;
+template <typename TI>
+__device__ __forceinline__ void unpack_chunk(const Chunk<TI>& c, float* out) {
+    if constexpr (sizeof(TI) == 4) {
+        const f32x4 a = __builtin_bit_cast(f32x4, c.v[0]);
+        const f32x4 b = __builtin_bit_cast(f32x4, c.v[1]);
+        out[0] = a.x, out[1] = a.y, out[2] = a.z, out[3] = a.w;
+        out[4] = b.x, out[5] = b.y, out[6] = b.z, out[7] = b.w;
+    } else {
+        unpack8<TI>(c.v[0], out);
+    }
 }
 
 template <typename TO>
@@ -69,35 +75,64 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeParams p) {
     const int h = (int)(bh % p.H);
     const int64_t b = bh / p.H;
     const int n = NB > 0 ? NB : p.n;
-
-    float l[DTATTN_MAX_MERGE_BLOCKS];
-    float m = kNegInf;
-#pragma unroll
-    for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) {
-        if (i >= n) break;
-        l[i] = p.lse_blocks[i][b * p.bl_b + h * p.bl_h + s];
-        m = fmaxf(m, l[i]);
-    }
-    const float mb = m == kNegInf ? 0.f : m;
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) {
-        if (i >= n) break;
-        l[i] = __expf(l[i] - mb);
-        sum += l[i];
-    }
-    const float inv = sum > 0.f ? 1.f / sum : 0.f;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int64_t lse_off = b * p.bl_b + h * p.bl_h + s;
     const int64_t in_off = b * p.bo_b + h * p.bo_h + (int64_t)s * p.bo_s + c * 8;
-#pragma unroll
-    for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) {
-        if (i >= n) break;
-        const float w = l[i] * inv;
-        if (w == 0.f) continue;  // a block with LSE = -inf is a no-op (its O may be anything)
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // A block with weight 0 (LSE = -inf) adds nothing, whatever its O holds (NaN included).
+    auto add = [&](const Chunk<TI>& raw, float w) {
         float x[8];
-        load8<TI>(reinterpret_cast<const TI*>(p.o_blocks[i]) + in_off, x);
+        unpack_chunk<TI>(raw, x);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(w, x[e], acc[e]);
+        for (int e = 0; e < 8; ++e) acc[e] = w != 0.f ? __builtin_fmaf(w, x[e], acc[e]) : acc[e];
+    };
+    float m = kNegInf, sum = 0.f, mb;
+    if constexpr (NB > 0) {
+        // every LSE and O load of the thread in one memory round trip
+        float l[NB];
+        Chunk<TI> raw[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            l[i] = p.lse_blocks[i][lse_off];
+            raw[i] = load_chunk<TI>(reinterpret_cast<const TI*>(p.o_blocks[i]) + in_off);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keeps the scheduler from issuing the later loads after waits
+#pragma unroll
+        for (int i = 0; i < NB; ++i) m = fmaxf(m, l[i]);
+        mb = m == kNegInf ? 0.f : m;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            l[i] = __expf(l[i] - mb);
+            sum += l[i];
+        }
+        const float inv = sum > 0.f ? 1.f / sum : 0.f;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) add(raw[i], l[i] * inv);
+    } else {
+        // the n LSE values first, then the O chunks in batches of four loads in flight together
+        float l[DTATTN_MAX_MERGE_BLOCKS];
+#pragma unroll
+        for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) l[i] = i < n ? p.lse_blocks[i][lse_off] : kNegInf;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) m = fmaxf(m, l[i]);
+        mb = m == kNegInf ? 0.f : m;
+#pragma unroll
+        for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) {
+            l[i] = __expf(l[i] - mb);  // blocks past n have LSE -inf: weight 0
+            sum += l[i];
+        }
+        const float inv = sum > 0.f ? 1.f / sum : 0.f;
+#pragma unroll
+        for (int i0 = 0; i0 < DTATTN_MAX_MERGE_BLOCKS; i0 += 4) {
+            if (i0 >= n) break;
+            Chunk<TI> raw[4] = {};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)  // uniform guard: the loads of a batch issue back to back
+                if (i0 + j < n) raw[j] = load_chunk<TI>(reinterpret_cast<const TI*>(p.o_blocks[i0 + j]) + in_off);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) add(raw[j], l[i0 + j] * inv);
+        }
     }
     store8<TO>(reinterpret_cast<TO*>(p.o) + b * p.o_b + h * p.o_h + (int64_t)s * p.o_s + c * 8, acc);
     if (p.lse != nullptr && c == 0) p.lse[b * p.l_b + h * p.l_h + s] = sum > 0.f ? mb + __logf(sum) : kNegInf;
