@@ -104,6 +104,31 @@ __device__ __forceinline__ u32x4 ld16_nt(const void* p) {
 }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
+// Raw bits of 8 consecutive elements of type T (16 bytes, or 32 for fp32).  Loading chunks and
+// unpacking them in separate steps lets a thread put all of its loads in flight before any use.
+template <typename T>
+struct Chunk {
+    u32x4 v[sizeof(T) == 4 ? 2 : 1];
+};
+template <typename T, bool NT>
+__device__ __forceinline__ Chunk<T> load_chunk(const T* p) {
+    Chunk<T> c;
+    c.v[0] = NT ? ld16_nt(p) : ld16(p);
+    if constexpr (sizeof(T) == 4) c.v[1] = NT ? ld16_nt(p + 4) : ld16(p + 4);
+    return c;
+}
+template <typename T>
+__device__ __forceinline__ void unpack_chunk(const Chunk<T>& c, float* out) {
+    if constexpr (sizeof(T) == 4) {
+        const f32x4 a = __builtin_bit_cast(f32x4, c.v[0]);
+        const f32x4 b = __builtin_bit_cast(f32x4, c.v[1]);
+        out[0] = a.x, out[1] = a.y, out[2] = a.z, out[3] = a.w;
+        out[4] = b.x, out[5] = b.y, out[6] = b.z, out[7] = b.w;
+    } else {
+        unpack8<T>(c.v[0], out);
+    }
+}
+
 // Buffer resource over `bytes` bytes from `base` (raw, stride 0).  Loads at offsets >= bytes return
 // zeros instead of touching memory, which is how tile loads handle ragged tails.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

@@ -5,14 +5,17 @@
 //   amax = max|x|, inv = 448 / amax, code = e4m3fn_rne(float(x * inv)) saturated to +-448,
 //   descale = amax / 448 (amax == 0: inv = descale = 1).
 // Two launches, no atomics and no zero-initialised memory:
-//   1. fp8_absmax_partial_kernel: one workgroup per (b, h, slice of rows) writes the slice's max|x|.
+//   1. fp8_absmax_partial_kernel: one workgroup per (b, h, slice of 64 rows) writes the slice's max|x|.
 //   2. fp8_quantize_kernel: each workgroup reduces its head's slice maxima, then converts its slice
 //      with v_cvt_pk_fp8_f32 (round to nearest even) and writes 16 codes per thread per step.
+// HBM-bound: a thread puts all loads of a batch in flight before the first use (a slice of 64 rows
+// at D = 128 is one batch per thread), and the second pass reads x again, mostly from L2 / MALL.
 #include "dtattn_common.hpp"
 
 namespace dtattn {
 
-constexpr int kQuantRowsPerSlice = 256;
+constexpr int kQuantRowsPerSlice = 64;
+constexpr int kQuantBatch = 4;  // 16-byte chunks (pass 1) or 16-element groups (pass 2) per thread per batch
 
 struct QuantParams {
     const void* x;
@@ -24,18 +27,6 @@ struct QuantParams {
 };
 
 template <typename T>
-__device__ __forceinline__ void load_row8(const T* p, float* out) {
-    unpack8<T>(ld16(p), out);
-}
-template <>
-__device__ __forceinline__ void load_row8<float>(const float* p, float* out) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
-    out[0] = a.x, out[1] = a.y, out[2] = a.z, out[3] = a.w;
-    out[4] = b.x, out[5] = b.y, out[6] = b.z, out[7] = b.w;
-}
-
-template <typename T>
 __global__ void __launch_bounds__(256) fp8_absmax_partial_kernel(const QuantParams p) {
     __shared__ float wmax[4];
     const int slice = blockIdx.x;
@@ -44,14 +35,23 @@ __global__ void __launch_bounds__(256) fp8_absmax_partial_kernel(const QuantPara
     const T* xp = reinterpret_cast<const T*>(p.x) + b * p.xs_b + h * p.xs_h;
     const int cpr = p.D / 8;
     const int r0 = slice * kQuantRowsPerSlice;
-    const int r1 = min(p.S, r0 + kQuantRowsPerSlice);
+    const int total = (min(p.S, r0 + kQuantRowsPerSlice) - r0) * cpr;
     float m = 0.f;
-    for (int idx = threadIdx.x; idx < (r1 - r0) * cpr; idx += 256) {
-        const int r = r0 + idx / cpr, c = idx % cpr;
-        float v[8];
-        load_row8<T>(xp + (int64_t)r * p.xs_s + c * 8, v);
+    for (int base = 0; base < total; base += 256 * kQuantBatch) {
+        Chunk<T> raw[kQuantBatch] = {};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+        for (int k = 0; k < kQuantBatch; ++k) {
+            const int idx = base + k * 256 + (int)threadIdx.x;
+            if (idx < total) raw[k] = load_chunk<T, false>(xp + (int64_t)(r0 + idx / cpr) * p.xs_s + (idx % cpr) * 8);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the batch's loads are all in flight before the first use
+#pragma unroll
+        for (int k = 0; k < kQuantBatch; ++k) {
+            float v[8];
+            unpack_chunk<T>(raw[k], v);  // chunks past the slice are zeros
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+        }
     }
     m = wave_max(m);
     if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
@@ -76,30 +76,50 @@ __global__ void __launch_bounds__(256) fp8_quantize_kernel(const QuantParams p) 
             if (slice == 0) p.descale[bh] = m > 0.f ? m / 448.f : 1.f;
         }
     }
-    __syncthreads();
-    const float inv = s_inv;
     const T* xp = reinterpret_cast<const T*>(p.x) + b * p.xs_b + h * p.xs_h;
     uint8_t* yp = p.x8 + ((int64_t)bh * p.S) * p.D;
-    const int cpr = p.D / 16;  // 16 codes per thread per step
+    const int cpr = p.D / 16;  // 16 codes per thread per group
     const int r0 = slice * kQuantRowsPerSlice;
-    const int r1 = min(p.S, r0 + kQuantRowsPerSlice);
-    for (int idx = threadIdx.x; idx < (r1 - r0) * cpr; idx += 256) {
-        const int r = r0 + idx / cpr, c = idx % cpr;
-        float v[16];
-        load_row8<T>(xp + (int64_t)r * p.xs_s + c * 16, v);
-        load_row8<T>(xp + (int64_t)r * p.xs_s + c * 16 + 8, v + 8);
-        uint32_t w[4];
+    const int total = (min(p.S, r0 + kQuantRowsPerSlice) - r0) * cpr;
+    bool first = true;
+    for (int base = 0; base < total; base += 256 * kQuantBatch) {
+        Chunk<T> raw[kQuantBatch][2] = {};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float y[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = fminf(fmaxf(v[4 * k + e] * inv, -448.f), 448.f);
-            int packed = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
-            packed = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], packed, true);
-            w[k] = (uint32_t)packed;
+        for (int k = 0; k < kQuantBatch; ++k) {  // x is read for the last time: non-temporal
+            const int idx = base + k * 256 + (int)threadIdx.x;
+            if (idx < total) {
+                const T* src = xp + (int64_t)(r0 + idx / cpr) * p.xs_s + (idx % cpr) * 16;
+                raw[k][0] = load_chunk<T, true>(src);
+                raw[k][1] = load_chunk<T, true>(src + 8);
+            }
         }
-        st16(yp + (int64_t)r * p.D + c * 16, u32x4{w[0], w[1], w[2], w[3]});
+        __builtin_amdgcn_sched_barrier(0);
+        if (first) {  // the head's scale (the loads above do not depend on it)
+            __syncthreads();
+            first = false;
+        }
+        const float inv = s_inv;
+#pragma unroll
+        for (int k = 0; k < kQuantBatch; ++k) {
+            const int idx = base + k * 256 + (int)threadIdx.x;
+            if (idx >= total) continue;
+            float v[16];
+            unpack_chunk<T>(raw[k][0], v);
+            unpack_chunk<T>(raw[k][1], v + 8);
+            uint32_t w[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float y[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = fminf(fmaxf(v[4 * q + e] * inv, -448.f), 448.f);
+                int packed = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+                packed = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], packed, true);
+                w[q] = (uint32_t)packed;
+            }
+            st16(yp + (int64_t)(r0 + idx / cpr) * p.D + (idx % cpr) * 16, u32x4{w[0], w[1], w[2], w[3]});
+        }
     }
+    if (first) __syncthreads();  // every thread reaches the workgroup barrier exactly once
 }
 
 template <typename T>

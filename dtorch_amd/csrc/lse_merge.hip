@@ -22,30 +22,7 @@ struct MergeParams {
     int32_t H, S, n;
 };
 
-// Block outputs are read exactly once: non-temporal loads.  A chunk is the raw bits of 8 elements,
-// loaded before any of them is used so that a thread's loads are in flight together.
-template <typename TI>
-struct Chunk {
-    u32x4 v[sizeof(TI) == 4 ? 2 : 1];
-};
-template <typename TI>
-__device__ __forceinline__ Chunk<TI> load_chunk(const TI* p) {
-    Chunk<TI> c;
-    c.v[0] = ld16_nt(p);
-    if constexpr (sizeof(TI) == 4) c.v[1] = ld16_nt(p + 4);
-    return c;
-}
-template <typename TI>
-__device__ __forceinline__ void unpack_chunk(const Chunk<TI>& c, float* out) {
-    if constexpr (sizeof(TI) == 4) {
-        const f32x4 a = __builtin_bit_cast(f32x4, c.v[0]);
-        const f32x4 b = __builtin_bit_cast(f32x4, c.v[1]);
-        out[0] = a.x, out[1] = a.y, out[2] = a.z, out[3] = a.w;
-        out[4] = b.x, out[5] = b.y, out[6] = b.z, out[7] = b.w;
-    } else {
-        unpack8<TI>(c.v[0], out);
-    }
-}
+// Block outputs are read exactly once: non-temporal loads (load_chunk<TI, true>).
 
 template <typename TO>
 __device__ __forceinline__ void store8(TO* p, const float* in);
@@ -93,7 +70,7 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeParams p) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             l[i] = p.lse_blocks[i][lse_off];
-            raw[i] = load_chunk<TI>(reinterpret_cast<const TI*>(p.o_blocks[i]) + in_off);
+            raw[i] = load_chunk<TI, true>(reinterpret_cast<const TI*>(p.o_blocks[i]) + in_off);
         }
         __builtin_amdgcn_sched_barrier(0);  // keeps the scheduler from issuing the later loads after waits
 #pragma unroll
@@ -128,7 +105,7 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeParams p) {
             Chunk<TI> raw[4] = {};
 #pragma unroll
             for (int j = 0; j < 4; ++j)  // uniform guard: the loads of a batch issue back to back
-                if (i0 + j < n) raw[j] = load_chunk<TI>(reinterpret_cast<const TI*>(p.o_blocks[i0 + j]) + in_off);
+                if (i0 + j < n) raw[j] = load_chunk<TI, true>(reinterpret_cast<const TI*>(p.o_blocks[i0 + j]) + in_off);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) add(raw[j], l[i0 + j] * inv);

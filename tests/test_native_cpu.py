@@ -117,7 +117,7 @@ def test_workspace_sizes():
     assert lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 0) == n  # default chunk 128
     lib.dtattn_fp8_quantize_workspace_size.restype = ctypes.c_size_t
     lib.dtattn_fp8_quantize_workspace_size.argtypes = [ctypes.c_int64] * 4
-    assert lib.dtattn_fp8_quantize_workspace_size(1, 24, 4608, 128) == ((24 * 18 * 4 + 255) // 256) * 256
+    assert lib.dtattn_fp8_quantize_workspace_size(1, 24, 4608, 128) == ((24 * 72 * 4 + 255) // 256) * 256  # 64-row slices
 
 
 def test_decode_paged_validation():
