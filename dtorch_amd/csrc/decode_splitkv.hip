@@ -73,10 +73,10 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int split = blockIdx.x;
-    const int hk = blockIdx.y % p.Hkv;
-    const int sg = blockIdx.y / p.Hkv;   // head subgroup within the kv group
-    const int b = blockIdx.z;
+    const int split = blockIdx.z;
+    const int hk = blockIdx.x % p.Hkv;
+    const int sg = blockIdx.x / p.Hkv;   // head subgroup within the kv group
+    const int b = blockIdx.y;
     const int L = min(max(p.lengths[b], 0), p.S_max);  // never read past the cache
     const int ns = (L + C - 1) / C;      // chunks of this sequence
     const int t0 = split * C;
@@ -301,7 +301,10 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p)
 
 template <typename T, int D, int G, int TPW, bool PAGED>
 static int launch_decode(const DecodeParams& p, hipStream_t stream) {
-    dim3 grid((unsigned)p.nsplit, (unsigned)(p.Hkv * (p.group / G)), (unsigned)p.B);
+    // Split index slowest: workgroups dispatched together read the same chunk of many sequences (and
+    // the empty chunks of short sequences gather at the end of the grid).  Measured against split
+    // fastest: +4% on random lengths, +31% on equal lengths of 4428 tokens.
+    dim3 grid((unsigned)(p.Hkv * (p.group / G)), (unsigned)p.B, (unsigned)p.nsplit);
     hipLaunchKernelGGL((decode_kernel<T, D, G, TPW, PAGED>), grid, dim3(256), 0, stream, p);
     int st = check_launch("decode_kernel");
     if (st != DTATTN_OK) return st;
