@@ -100,7 +100,8 @@ typedef struct {
     int64_t lse_stride[1]; /* B (H stride is 1) */
     int32_t dtype;         /* BF16 or FP16 */
     float scale;           /* <= 0 means 1/sqrt(D) */
-    int32_t chunk;         /* tokens per split: 128, 256 or 512; 0 picks the default (128) */
+    int32_t chunk;         /* tokens per split: 128, 256 or 512; 0 picks 256 (128 when Hq / Hkv is a
+                              multiple of 8); workspace sizes for chunk 0 cover either choice */
     void* workspace;       /* >= dtattn_decode_workspace_size(...) bytes, 256-byte aligned */
     size_t workspace_bytes;
 } dtattn_decode_args;
@@ -134,7 +135,7 @@ typedef struct {
     int64_t block_table_stride;/* elements between rows of block_table */
     int32_t dtype;             /* BF16 or FP16 */
     float scale;               /* <= 0 means 1/sqrt(D) */
-    int32_t chunk;             /* tokens per split: 128, 256 or 512; 0 picks the default (128) */
+    int32_t chunk;             /* tokens per split: 128, 256 or 512; 0 picks as dtattn_decode_args does */
     void* workspace;           /* >= dtattn_decode_paged_workspace_size(...) bytes, 256-byte aligned */
     size_t workspace_bytes;
 } dtattn_decode_paged_args;
