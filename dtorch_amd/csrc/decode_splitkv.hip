@@ -45,11 +45,11 @@ struct DecodeParams {
 
 constexpr int kDecodeChunk = 128;  // smallest split; workspace queries with chunk 0 size for it
 
-// Split length picked for chunk = 0: 256 tokens, or 128 when the query heads per kv head are a
-// multiple of 8 (8 heads per workgroup leave no registers for 256-token splits).  Measured on one
-// MI355X over batch 1-128, contexts 2K-128K: 256 was best or within 2% for groups of 1-4; for
-// groups of 8 (Hq 64, Hkv 8) 128 streamed 2.7 TB/s against 1.9-2.1 TB/s.
-static int32_t auto_chunk(int64_t Hq, int64_t Hkv) { return (Hq / Hkv) % 8 == 0 ? 128 : 256; }
+// Split length picked for chunk = 0: 256 tokens, or 128 for the 8-head workgroups (8 heads per
+// workgroup leave no registers for 256-token splits).  Measured on one MI355X over batch 1-128,
+// contexts 2K-128K: 256 was best or within 2% for 1-4 heads per workgroup; with 8 heads per
+// workgroup 128 streamed 3.0 TB/s against 2.1-2.3 TB/s.
+static int32_t auto_chunk(int64_t Hq, int64_t Hkv) { return (Hq / Hkv) % 8 == 0 && Hkv % 8 != 0 ? 128 : 256; }
 
 size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk, int64_t* nsplit_out) {
     const int64_t nsplit = (S_max + chunk - 1) / chunk;
@@ -332,7 +332,11 @@ static int dispatch_chunk(const DecodeParams& p, hipStream_t stream) {
 template <typename T, int D, bool PAGED>
 static int dispatch_group(const DecodeParams& p, hipStream_t stream) {
     const int g = p.group;
-    if (g % 8 == 0) return dispatch_chunk<T, D, 8, PAGED>(p, stream);
+    // Groups of 8 heads: with Hkv a multiple of 8 the two 4-head subgroups of a kv head have workgroup
+    // ids 8 apart, i.e. run on the same XCD, so the second read of each chunk hits that XCD's L2 and
+    // the lighter 4-head kernel takes 256-token splits (measured +5-13% at Hq 64, Hkv 8); otherwise
+    // one 8-head workgroup reads the chunk once.
+    if (g % 8 == 0 && p.Hkv % 8 != 0) return dispatch_chunk<T, D, 8, PAGED>(p, stream);
     if (g % 4 == 0) return dispatch_chunk<T, D, 4, PAGED>(p, stream);
     if (g % 2 == 0) return dispatch_chunk<T, D, 2, PAGED>(p, stream);
     return dispatch_chunk<T, D, 1, PAGED>(p, stream);

@@ -101,7 +101,7 @@ typedef struct {
     int32_t dtype;         /* BF16 or FP16 */
     float scale;           /* <= 0 means 1/sqrt(D) */
     int32_t chunk;         /* tokens per split: 128, 256 or 512; 0 picks 256 (128 when Hq / Hkv is a
-                              multiple of 8); workspace sizes for chunk 0 cover either choice */
+                              multiple of 8 and Hkv is not); workspace sizes for chunk 0 cover it */
     void* workspace;       /* >= dtattn_decode_workspace_size(...) bytes, 256-byte aligned */
     size_t workspace_bytes;
 } dtattn_decode_args;

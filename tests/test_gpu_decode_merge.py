@@ -36,6 +36,7 @@ def _decode_case(B, Hq, Hkv, Smax, D, lengths, chunk=0, dtype=torch.bfloat16, se
     (3, 32, 8, 1024, 128, [1, 256, 1024], 0),
     (4, 8, 8, 600, 128, [255, 257, 511, 600], 0),    # MHA, chunk boundaries
     (2, 16, 2, 700, 128, [700, 129], 128),            # GQA 8
+    (2, 64, 8, 600, 128, [600, 257], 0),              # GQA 8 with Hkv 8: two 4-head workgroups per kv head
     (2, 12, 2, 300, 128, [300, 77], 0),               # GQA 6 -> subgroups of 2
     (2, 8, 4, 520, 64, [519, 3], 512),                # D = 64, chunk 512
 ])
@@ -267,6 +268,7 @@ def _gather_dev(pool, bt, lengths, S):
     (128, 2, 16, 2, 128, [700, 129], 256, True),         # GQA 8, token-major pool
     (256, 2, 12, 2, 128, [1000, 77], 512, False),        # GQA 6
     (16, 2, 8, 4, 64, [519, 3], 128, True),              # D = 64
+    (32, 2, 64, 8, 128, [600, 40], 0, False),            # GQA 8 with Hkv 8
 ])
 def test_decode_paged_small(ps, B, Hq, Hkv, D, lengths, chunk, token_major):
     rng = np.random.default_rng(ps + B)
