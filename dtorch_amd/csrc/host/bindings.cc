@@ -86,6 +86,18 @@ PYBIND11_MODULE(_dtattn_host, m) {
             return RunCompute([&](const TorchTensorOptArray& i, TorchTensorArray& o) { op.Compute(i, o); }, in);
         });
 
+    py::class_<KvCacheAppendOp>(m, "KvCacheAppendOp")
+        .def(py::init<>())
+        .def("compute", [](const KvCacheAppendOp& op, const std::vector<std::optional<at::Tensor>>& in) {
+            return RunCompute([&](const TorchTensorOptArray& i, TorchTensorArray& o) { op.Compute(i, o); }, in);
+        });
+
+    py::class_<KvCacheAppendPagedOp>(m, "KvCacheAppendPagedOp")
+        .def(py::init<>())
+        .def("compute", [](const KvCacheAppendPagedOp& op, const std::vector<std::optional<at::Tensor>>& in) {
+            return RunCompute([&](const TorchTensorOptArray& i, TorchTensorArray& o) { op.Compute(i, o); }, in);
+        });
+
     py::class_<LseMergeOp>(m, "LseMergeOp")
         .def(py::init<std::optional<c10::ScalarType>>(), py::arg("out_dtype") = std::nullopt)
         .def("compute", [](const LseMergeOp& op, const std::vector<std::optional<at::Tensor>>& in) {

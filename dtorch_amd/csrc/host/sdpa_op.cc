@@ -323,6 +323,108 @@ void SdpaDecodeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& 
     outputs.push_back(lse);
 }
 
+namespace {
+
+// A cache written in place: it cannot be copied to fix its layout, so the layout is checked instead.
+void CheckCacheLayout(const at::Tensor& c, const char* name) {
+    if (c.dim() != 4) Throw(std::string(name) + " must be 4-D");
+    if (c.stride(3) != 1) Throw(std::string(name) + " needs a unit stride along D");
+    for (int i = 0; i < 3; ++i)
+        if ((c.stride(i) * c.element_size()) % 16 != 0)
+            Throw(std::string(name) + " strides must be multiples of 16 bytes (it is updated in place)");
+    if ((reinterpret_cast<uintptr_t>(c.data_ptr()) & 15u) != 0) Throw(std::string(name) + " must be 16-byte aligned");
+}
+
+struct NewTokens {
+    View4 k, v;
+};
+
+NewTokens CheckNewTokens(const at::Tensor& kn, const at::Tensor& vn, const at::Tensor& kc, int64_t B, int64_t Hkv,
+                         int64_t D) {
+    if (kn.dim() != 4 || vn.dim() != 4 || kn.sizes() != vn.sizes())
+        Throw("k_new and v_new must be 4-D tensors of the same shape [B, Hkv, n_new, D]");
+    if (kn.size(0) != B || kn.size(1) != Hkv || kn.size(3) != D)
+        Throw("k_new must be [B, Hkv, n_new, D] matching the cache");
+    if (kn.scalar_type() != kc.scalar_type() || vn.scalar_type() != kc.scalar_type())
+        Throw("new tokens and cache dtypes differ");
+    if (kc.scalar_type() != at::kBFloat16 && kc.scalar_type() != at::kHalf) Throw("the KV cache must be bf16 or fp16");
+    NewTokens r;
+    r.k = MakeView4(kn, "k_new");
+    r.v = MakeView4(vn, "v_new");
+    return r;
+}
+
+void CheckLengths(const at::Tensor& len, int64_t B) {
+    if (len.scalar_type() != at::kInt || len.dim() != 1 || len.size(0) != B || !len.is_contiguous())
+        Throw("lengths must be a contiguous int32 tensor of shape [B] (it is updated in place)");
+}
+
+}  // namespace
+
+void KvCacheAppendOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
+    if (inputs.size() != 5 || !inputs[0] || !inputs[1] || !inputs[2] || !inputs[3] || !inputs[4])
+        Throw("KvCacheAppendOp expects 5 inputs {k_cache, v_cache, lengths, k_new, v_new}");
+    const at::Tensor &kc = *inputs[0], &vc = *inputs[1], &len = *inputs[2], &kn = *inputs[3], &vn = *inputs[4];
+    CheckDevice({&kc, &vc, &len, &kn, &vn});
+    c10::DeviceGuard guard(kc.device());
+    CheckCacheLayout(kc, "k_cache");
+    CheckCacheLayout(vc, "v_cache");
+    if (kc.sizes() != vc.sizes()) Throw("k_cache and v_cache shapes differ");
+    if (vc.scalar_type() != kc.scalar_type()) Throw("k_cache and v_cache dtypes differ");
+    const int64_t B = kc.size(0), Hkv = kc.size(1), S_max = kc.size(2), D = kc.size(3);
+    CheckLengths(len, B);
+    NewTokens nt = CheckNewTokens(kn, vn, kc, B, Hkv, D);
+    dtattn_kv_append_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.k_new = nt.k.t.data_ptr(), a.v_new = nt.v.t.data_ptr();
+    a.k_cache = kc.data_ptr(), a.v_cache = vc.data_ptr();
+    a.lengths = len.data_ptr<int32_t>();
+    a.B = B, a.Hkv = Hkv, a.n_new = kn.size(2), a.S_max = S_max, a.D = D;
+    a.k_new_stride[0] = nt.k.sb, a.k_new_stride[1] = nt.k.sh, a.k_new_stride[2] = nt.k.ss;
+    a.v_new_stride[0] = nt.v.sb, a.v_new_stride[1] = nt.v.sh, a.v_new_stride[2] = nt.v.ss;
+    for (int i = 0; i < 3; ++i) a.k_stride[i] = kc.stride(i), a.v_stride[i] = vc.stride(i);
+    a.dtype = DtypeCode(kc.scalar_type());
+    Check(dtattn_kv_append(&a, CurrentStream(kc)), "dtattn_kv_append");
+    outputs.push_back(kc);
+    outputs.push_back(vc);
+    outputs.push_back(len);
+}
+
+void KvCacheAppendPagedOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
+    if (inputs.size() != 6 || !inputs[0] || !inputs[1] || !inputs[2] || !inputs[3] || !inputs[4] || !inputs[5])
+        Throw("KvCacheAppendPagedOp expects 6 inputs {k_pages, v_pages, block_table, lengths, k_new, v_new}");
+    const at::Tensor &kp = *inputs[0], &vp = *inputs[1], &bt = *inputs[2], &len = *inputs[3], &kn = *inputs[4],
+                     &vn = *inputs[5];
+    CheckDevice({&kp, &vp, &bt, &len, &kn, &vn});
+    c10::DeviceGuard guard(kp.device());
+    CheckCacheLayout(kp, "k_pages");
+    CheckCacheLayout(vp, "v_pages");
+    if (kp.sizes() != vp.sizes()) Throw("k_pages and v_pages shapes differ");
+    if (vp.scalar_type() != kp.scalar_type()) Throw("k_pages and v_pages dtypes differ");
+    if (bt.scalar_type() != at::kInt || bt.dim() != 2) Throw("block_table must be an int32 tensor of shape [B, max_pages]");
+    const int64_t B = bt.size(0), Hkv = kp.size(1), D = kp.size(3);
+    CheckLengths(len, B);
+    NewTokens nt = CheckNewTokens(kn, vn, kp, B, Hkv, D);
+    at::Tensor btc = bt.stride(1) == 1 ? bt : bt.contiguous();
+    dtattn_kv_append_paged_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.k_new = nt.k.t.data_ptr(), a.v_new = nt.v.t.data_ptr();
+    a.k_pages = kp.data_ptr(), a.v_pages = vp.data_ptr();
+    a.block_table = btc.data_ptr<int32_t>();
+    a.lengths = len.data_ptr<int32_t>();
+    a.B = B, a.Hkv = Hkv, a.n_new = kn.size(2), a.D = D;
+    a.num_pages = kp.size(0), a.page_size = kp.size(2), a.max_pages = bt.size(1);
+    a.k_new_stride[0] = nt.k.sb, a.k_new_stride[1] = nt.k.sh, a.k_new_stride[2] = nt.k.ss;
+    a.v_new_stride[0] = nt.v.sb, a.v_new_stride[1] = nt.v.sh, a.v_new_stride[2] = nt.v.ss;
+    for (int i = 0; i < 3; ++i) a.k_stride[i] = kp.stride(i), a.v_stride[i] = vp.stride(i);
+    a.block_table_stride = btc.stride(0);
+    a.dtype = DtypeCode(kp.scalar_type());
+    Check(dtattn_kv_append_paged(&a, CurrentStream(kp)), "dtattn_kv_append_paged");
+    outputs.push_back(kp);
+    outputs.push_back(vp);
+    outputs.push_back(len);
+}
+
 void SdpaDecodePagedOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
     if (inputs.size() != 5 || !inputs[0] || !inputs[1] || !inputs[2] || !inputs[3] || !inputs[4])
         Throw("SdpaDecodePagedOp expects 5 inputs {query, k_pages, v_pages, block_table, lengths}");

@@ -124,6 +124,22 @@ private:
     int32_t mChunk;
 };
 
+// KV-cache append (no counterpart in the reference: its Llama port keeps no cache,
+// python/dtorch/test/modules/llama.py:126-156).  {k_cache, v_cache, lengths, k_new, v_new} ->
+// {k_cache, v_cache, lengths}, all three updated in place: token j of sequence b lands at position
+// lengths[b] + j (dropped at or past S_max), then lengths[b] += n_new, saturating at S_max.
+class KvCacheAppendOp {
+public:
+    void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
+};
+
+// The same for the paged cache of SdpaDecodePagedOp: {k_pages, v_pages, block_table, lengths, k_new,
+// v_new} -> {k_pages, v_pages, lengths}; the block table must already name the pages being written.
+class KvCacheAppendPagedOp {
+public:
+    void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
+};
+
 // {O_0, LSE_0, O_1, LSE_1, ...} -> {O, LSE}; O in `outDtype` (default: the blocks' dtype).
 class LseMergeOp {
 public:

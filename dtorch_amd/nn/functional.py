@@ -132,6 +132,24 @@ def decode_attention_paged(query: torch.Tensor, k_pages: torch.Tensor, v_pages: 
     return o, lse
 
 
+def kv_cache_append(k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor, k_new: torch.Tensor,
+                    v_new: torch.Tensor) -> None:
+    """Write n_new tokens per sequence into a [B, Hkv, S_max, D] cache, in place.
+
+    k_new / v_new are [B, Hkv, n_new, D] (any strides with unit stride on D, e.g. a transposed projection
+    output).  Token j of sequence b lands at position lengths[b] + j; positions at or past S_max are not
+    written.  lengths (contiguous int32 [B]) then advances by n_new, saturating at S_max.
+    """
+    _h.KvCacheAppendOp().compute([k_cache, v_cache, lengths, k_new, v_new])
+
+
+def kv_cache_append_paged(k_pages: torch.Tensor, v_pages: torch.Tensor, block_table: torch.Tensor,
+                          lengths: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+    """kv_cache_append for the paged cache of decode_attention_paged; the block table must already name
+    the pages of the positions being written."""
+    _h.KvCacheAppendPagedOp().compute([k_pages, v_pages, block_table, lengths, k_new, v_new])
+
+
 def lse_merge(outs: Sequence[torch.Tensor], lses: Sequence[torch.Tensor],
               out_dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Merge partial attention blocks over the same queries by their LSE."""

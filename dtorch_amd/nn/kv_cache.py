@@ -1,0 +1,112 @@
+"""KV caches for the decode loop: a padded per-sequence cache and a paged one.
+
+The reference's Llama port keeps no cache and recomputes causal attention over the whole sequence at
+every step (python/dtorch/test/modules/llama.py:126-156, with repeat_kv for GQA at :80-85).  These
+classes hold the keys and values of the tokens seen so far, so that a step appends its new tokens and
+attends with the split-KV decode kernels:
+
+    cache = KVCache(batch, kv_heads, max_len, head_dim)
+    out = cache.prefill(q, k, v)          # prompt: causal attention, then its K/V into the cache
+    out = cache.decode(q1, k1, v1)        # one token per sequence: append, then decode attention
+
+Prompts in one prefill call share their length; per-sequence lengths then diverge only through the
+caller's own use of `lengths`.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import functional as F
+
+
+class KVCache:
+    """Padded cache [B, Hkv, max_len, D] plus device lengths [B] (int32)."""
+
+    def __init__(self, batch: int, kv_heads: int, max_len: int, head_dim: int, dtype=torch.bfloat16,
+                 device="cuda", scale: Optional[float] = None):
+        self.k = torch.zeros(batch, kv_heads, max_len, head_dim, dtype=dtype, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.lengths = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.scale = scale
+        self._host_len = np.zeros(batch, dtype=np.int64)  # mirrors `lengths` for capacity checks
+
+    @property
+    def capacity(self) -> int:
+        return self.k.shape[2]
+
+    def _reserve(self, n: int) -> None:
+        if int(self._host_len.max(initial=0)) + n > self.capacity:
+            raise ValueError(f"KV cache full: {int(self._host_len.max())} + {n} tokens > capacity {self.capacity}")
+        self._host_len += n
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+        """Append [B, Hkv, n, D] keys and values after each sequence's current length."""
+        self._reserve(k_new.shape[2])
+        F.kv_cache_append(self.k, self.v, self.lengths, k_new, v_new)
+
+    def prefill(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """Causal attention over a prompt of equal length per sequence (the cache must be empty for the
+        causal alignment to hold), then the prompt's K/V into the cache."""
+        if int(self._host_len.max(initial=0)) != 0:
+            raise ValueError("prefill expects an empty cache; use decode() for later tokens")
+        out = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=self.scale, enable_gqa=True)
+        self.append(k, v)
+        return out
+
+    def decode(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> torch.Tensor:
+        """One new token per sequence: append its K/V, then attend over everything cached."""
+        self.append(k_new, v_new)
+        return F.decode_attention(q, self.k, self.v, self.lengths, scale=self.scale)[0]
+
+
+class PagedKVCache:
+    """Paged cache: pools [num_pages, Hkv, page_size, D], a block table [B, max_pages] and lengths [B].
+
+    Pages come from a host-side free list when a sequence's next tokens cross into a new page; the block
+    table rows that change are copied to the device before the append that writes them.
+    """
+
+    def __init__(self, batch: int, kv_heads: int, num_pages: int, page_size: int, max_pages: int, head_dim: int,
+                 dtype=torch.bfloat16, device="cuda", scale: Optional[float] = None):
+        self.k = torch.zeros(num_pages, kv_heads, page_size, head_dim, dtype=dtype, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.page_size = page_size
+        self.scale = scale
+        self._free = list(range(num_pages - 1, -1, -1))
+        self._table = np.zeros((batch, max_pages), dtype=np.int32)
+        self._pages = np.zeros(batch, dtype=np.int64)  # pages assigned per sequence
+        self._host_len = np.zeros(batch, dtype=np.int64)
+        self.block_table = torch.from_numpy(self._table).to(device)
+        self.lengths = torch.zeros(batch, dtype=torch.int32, device=device)
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+        n = k_new.shape[2]
+        need = (self._host_len + n + self.page_size - 1) // self.page_size
+        if int(need.max(initial=0)) > self._table.shape[1]:
+            raise ValueError("PagedKVCache: a sequence exceeds max_pages * page_size tokens")
+        if int((need - self._pages).sum()) > len(self._free):
+            raise ValueError("PagedKVCache: out of pages")
+        changed = False
+        for b in range(len(need)):
+            while self._pages[b] < need[b]:
+                self._table[b, self._pages[b]] = self._free.pop()
+                self._pages[b] += 1
+                changed = True
+        if changed:
+            self.block_table.copy_(torch.from_numpy(self._table), non_blocking=False)
+        self._host_len += n
+        F.kv_cache_append_paged(self.k, self.v, self.block_table, self.lengths, k_new, v_new)
+
+    def prefill(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        if int(self._host_len.max(initial=0)) != 0:
+            raise ValueError("prefill expects an empty cache; use decode() for later tokens")
+        out = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=self.scale, enable_gqa=True)
+        self.append(k, v)
+        return out
+
+    def decode(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> torch.Tensor:
+        self.append(k_new, v_new)
+        return F.decode_attention_paged(q, self.k, self.v, self.block_table, self.lengths, scale=self.scale)[0]

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define DTATTN_ABI_VERSION 2
+#define DTATTN_ABI_VERSION 3
 
 typedef enum {
     DTATTN_OK = 0,
@@ -143,6 +143,54 @@ typedef struct {
 size_t dtattn_decode_paged_workspace_size(int64_t B, int64_t Hq, int64_t max_pages, int64_t page_size, int64_t D,
                                           int32_t chunk);
 int dtattn_decode_paged(const dtattn_decode_paged_args* args, void* stream);
+
+/* KV-cache append: writes the new tokens' keys and values into the cache that the decode entry points
+ * read.
+ *
+ * No counterpart in the reference (its Llama port keeps no cache and recomputes attention over the whole
+ * sequence each step, python/dtorch/test/modules/llama.py:126-156); the write side of the decode loop
+ * listed as the next step for decode.  Token j (0 <= j < n_new) of sequence b goes to cache position
+ * t = max(lengths[b], 0) + j; positions at or past the capacity are not written.  Afterwards, in stream
+ * order, lengths[b] = min(max(lengths[b], 0) + n_new, capacity): callers that must not drop tokens check
+ * the capacity on the host.  dtype BF16 or FP16 for new tokens and cache alike; D a multiple of 8.
+ */
+typedef struct {
+    const void* k_new;     /* [B, Hkv, n_new, D] (any strides, D stride 1) */
+    const void* v_new;
+    void* k_cache;         /* [B, Hkv, S_max, D]; capacity S_max */
+    void* v_cache;
+    int32_t* lengths;      /* [B] device int32, read and then advanced */
+    int64_t B, Hkv, n_new, S_max, D;
+    int64_t k_new_stride[3]; /* B, H, token */
+    int64_t v_new_stride[3];
+    int64_t k_stride[3];     /* B, H, S */
+    int64_t v_stride[3];
+    int32_t dtype;
+} dtattn_kv_append_args;
+
+int dtattn_kv_append(const dtattn_kv_append_args* args, void* stream);
+
+/* The same for a paged cache laid out as dtattn_decode_paged reads it: position t of sequence b is row
+ * t % page_size of page block_table[b][t / page_size] (page ids clamped to [0, num_pages)); capacity
+ * max_pages * page_size.  The caller assigns the pages of the positions being written beforehand. */
+typedef struct {
+    const void* k_new;         /* [B, Hkv, n_new, D] (any strides, D stride 1) */
+    const void* v_new;
+    void* k_pages;             /* page pool, e.g. [num_pages, Hkv, page_size, D] (any strides below) */
+    void* v_pages;
+    const int32_t* block_table;/* [B, max_pages] device int32 */
+    int32_t* lengths;          /* [B] device int32, read and then advanced */
+    int64_t B, Hkv, n_new, D;
+    int64_t num_pages, page_size, max_pages;  /* page_size: a power of two >= 16 */
+    int64_t k_new_stride[3];
+    int64_t v_new_stride[3];
+    int64_t k_stride[3];       /* page, H, row within the page */
+    int64_t v_stride[3];
+    int64_t block_table_stride;
+    int32_t dtype;
+} dtattn_kv_append_paged_args;
+
+int dtattn_kv_append_paged(const dtattn_kv_append_paged_args* args, void* stream);
 
 /* LSE merge of n partial attention blocks over the same queries.
  *

@@ -23,7 +23,9 @@ defined by their closed forms (LSE_i = log sum_j exp(scale q_i.k_j) over unmaske
 LSE = m + log sum_b exp(LSE_b - m), O = sum_b exp(LSE_b - LSE) O_b).  ``q_offset``/``k_offset``
 generalise the causal alignment: key j is visible to query i iff ``j + k_offset <= i + q_offset``
 (0, 0 is torch's top-left alignment).  A query row that sees no key gets O = 0 and LSE = -inf, so
-that it is a no-op in a merge.
+that it is a no-op in a merge.  The KV-cache append (``kv_append``, ``kv_append_paged``) is a copy into
+the positions after each sequence's length; tests pin it by round trips (a sequence appended in pieces
+equals the sequence, and decode over the appended cache equals causal attention over the full one).
 """
 from __future__ import annotations
 
@@ -153,6 +155,38 @@ def decode_paged(q, k_pages, v_pages, block_table, lengths, scale: Optional[floa
     kc = gather_pages(k_pages, block_table, lengths)
     vc = gather_pages(v_pages, block_table, lengths)
     return decode(q, kc, vc, lengths, scale=scale)
+
+
+def kv_append(cache, lengths, new):
+    """KV-cache append (new path, no reference function: the reference keeps no cache,
+    python/dtorch/test/modules/llama.py:126-156).  cache [B, H, S_max, D] and lengths [B] are updated in
+    place: token j of sequence b goes to position max(lengths[b], 0) + j unless that is >= S_max, then
+    lengths[b] = min(max(lengths[b], 0) + n_new, S_max).  new is [B, H, n_new, D]."""
+    s_max = cache.shape[2]
+    n_new = new.shape[2]
+    for b in range(cache.shape[0]):
+        t0 = max(int(lengths[b]), 0)
+        n = max(0, min(n_new, s_max - t0))
+        cache[b, :, t0:t0 + n] = new[b, :, :n]
+        lengths[b] = min(t0 + n_new, s_max)
+
+
+def kv_append_paged(pages, block_table, lengths, new):
+    """kv_append for a paged cache: position t of sequence b is row t % page_size of page
+    block_table[b, t // page_size] (clamped to the pool) in pages [num_pages, H, page_size, D]; the capacity
+    is max_pages * page_size.  pages and lengths are updated in place."""
+    num_pages, _, ps, _ = pages.shape
+    cap = block_table.shape[1] * ps
+    n_new = new.shape[2]
+    for b in range(block_table.shape[0]):
+        t0 = max(int(lengths[b]), 0)
+        for j in range(n_new):
+            t = t0 + j
+            if t >= cap:
+                break
+            page = min(max(int(block_table[b, t // ps]), 0), num_pages - 1)
+            pages[page, :, t % ps] = new[b, :, j]
+        lengths[b] = min(t0 + n_new, cap)
 
 
 def lse_merge(os: Sequence[np.ndarray], lses: Sequence[np.ndarray]) -> Tuple[np.ndarray, np.ndarray]:

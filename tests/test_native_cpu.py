@@ -32,7 +32,7 @@ def declared_functions():
 def test_header_declares_the_abi():
     names = declared_functions()
     for n in ["dtattn_prefill_fwd", "dtattn_decode_splitkv", "dtattn_decode_workspace_size", "dtattn_decode_paged",
-              "dtattn_decode_paged_workspace_size", "dtattn_lse_merge",
+              "dtattn_decode_paged_workspace_size", "dtattn_kv_append", "dtattn_kv_append_paged", "dtattn_lse_merge",
               "dtattn_fp8_quantize_per_head", "dtattn_fp8_quantize_workspace_size", "dtattn_get_device_peaks",
               "dtattn_last_error", "dtattn_abi_version"]:
         assert n in names
@@ -148,6 +148,57 @@ def test_decode_paged_validation():
     # the paged workspace is the padded one for S_max = max_pages * page_size
     assert lib.dtattn_decode_paged_workspace_size(64, 32, 512, 16, 128, 0) == \
         lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 0)
+
+
+class AppendArgs(ctypes.Structure):
+    _fields_ = [("k_new", ctypes.c_void_p), ("v_new", ctypes.c_void_p), ("k_cache", ctypes.c_void_p),
+                ("v_cache", ctypes.c_void_p), ("lengths", ctypes.c_void_p), ("B", ctypes.c_int64),
+                ("Hkv", ctypes.c_int64), ("n_new", ctypes.c_int64), ("S_max", ctypes.c_int64), ("D", ctypes.c_int64),
+                ("k_new_stride", ctypes.c_int64 * 3), ("v_new_stride", ctypes.c_int64 * 3),
+                ("k_stride", ctypes.c_int64 * 3), ("v_stride", ctypes.c_int64 * 3), ("dtype", ctypes.c_int32)]
+
+
+class AppendPagedArgs(ctypes.Structure):
+    _fields_ = [("k_new", ctypes.c_void_p), ("v_new", ctypes.c_void_p), ("k_pages", ctypes.c_void_p),
+                ("v_pages", ctypes.c_void_p), ("block_table", ctypes.c_void_p), ("lengths", ctypes.c_void_p),
+                ("B", ctypes.c_int64), ("Hkv", ctypes.c_int64), ("n_new", ctypes.c_int64), ("D", ctypes.c_int64),
+                ("num_pages", ctypes.c_int64), ("page_size", ctypes.c_int64), ("max_pages", ctypes.c_int64),
+                ("k_new_stride", ctypes.c_int64 * 3), ("v_new_stride", ctypes.c_int64 * 3),
+                ("k_stride", ctypes.c_int64 * 3), ("v_stride", ctypes.c_int64 * 3),
+                ("block_table_stride", ctypes.c_int64), ("dtype", ctypes.c_int32)]
+
+
+def test_kv_append_validation():
+    # every case fails validation before any launch (no pointer here is dereferenced)
+    lib.dtattn_kv_append.restype = ctypes.c_int
+    lib.dtattn_kv_append_paged.restype = ctypes.c_int
+    assert lib.dtattn_kv_append(None, None) == 1
+    a = AppendArgs()
+    a.B, a.Hkv, a.n_new, a.S_max, a.D = 2, 2, 1, 64, 128
+    a.dtype = 2  # fp8 is not a cache dtype
+    assert lib.dtattn_kv_append(ctypes.byref(a), None) == 2 and "dtype" in _last_error()
+    a.dtype, a.D = 0, 12
+    assert lib.dtattn_kv_append(ctypes.byref(a), None) == 2 and "multiple of 8" in _last_error()
+    a.D = 128
+    assert lib.dtattn_kv_append(ctypes.byref(a), None) == 1 and "null" in _last_error()
+    a.k_new = a.v_new = a.lengths = 4096  # never dereferenced: the stride check fails first
+    for arr in (a.k_new_stride, a.v_new_stride, a.k_stride, a.v_stride):
+        arr[0], arr[1], arr[2] = 2 * 64 * 128, 64 * 128, 128
+    a.k_stride[2] = 100
+    assert lib.dtattn_kv_append(ctypes.byref(a), None) == 2 and "16 bytes" in _last_error()
+    a.k_stride[2] = 128
+    a.k_new = 4104  # not 16-byte aligned
+    assert lib.dtattn_kv_append(ctypes.byref(a), None) == 2 and "aligned" in _last_error()
+    a.k_new, a.S_max = 4096, 0
+    assert lib.dtattn_kv_append(ctypes.byref(a), None) == 1 and "S_max" in _last_error()
+    p = AppendPagedArgs()
+    p.B, p.Hkv, p.n_new, p.D, p.num_pages, p.max_pages, p.page_size = 2, 2, 1, 128, 8, 4, 24
+    p.k_new = p.v_new = p.lengths = 4096
+    for arr in (p.k_new_stride, p.v_new_stride, p.k_stride, p.v_stride):
+        arr[0], arr[1], arr[2] = 2 * 64 * 128, 64 * 128, 128
+    assert lib.dtattn_kv_append_paged(ctypes.byref(p), None) == 1 and "page_size" in _last_error()
+    p.page_size, p.num_pages = 16, 0
+    assert lib.dtattn_kv_append_paged(ctypes.byref(p), None) == 1 and "page counts" in _last_error()
 
 
 def test_merge_validation():

@@ -323,3 +323,40 @@ def test_planted_mistakes_are_caught():
     # 7. fp8 round-half-up instead of half-to-even differs from torch at ties
     tie = np.float32(1.0625)  # between 1.0 and 1.125: even mantissa is 1.0
     assert orc.e4m3fn_decode(orc.e4m3fn_encode(np.array([tie])))[0] == 1.0
+
+
+def test_kv_append_round_trip_and_capacity():
+    # appending a sequence in pieces reproduces it; positions past S_max are dropped and lengths saturate
+    rng = np.random.default_rng(31)
+    B, H, S, D = 3, 2, 40, 8
+    full = rng.standard_normal((B, H, S, D))
+    cache = np.zeros((B, H, 32, D))
+    lengths = np.array([0, 5, -3], dtype=np.int64)  # a negative length counts as 0
+    start = np.maximum(lengths, 0).copy()
+    pos = 0
+    for n in (1, 7, 3, 30):
+        orc.kv_append(cache, lengths, full[:, :, pos:pos + n])
+        pos += n
+    for b in range(B):
+        n_in = min(32 - start[b], S)
+        assert np.array_equal(cache[b, :, start[b]:start[b] + n_in], full[b, :, :n_in])
+        assert lengths[b] == min(start[b] + 41, 32)
+    assert np.all(cache[1, :, :5] == 0)  # rows before the starting length untouched
+
+
+def test_kv_append_paged_matches_contiguous():
+    rng = np.random.default_rng(32)
+    B, H, D, ps, max_pages = 3, 2, 8, 16, 3
+    P = B * max_pages + 2
+    table = rng.permutation(P)[:B * max_pages].reshape(B, max_pages).astype(np.int32)
+    pages = np.zeros((P, H, ps, D))
+    contig = np.zeros((B, H, max_pages * ps, D))
+    lp = np.array([0, 3, 17], dtype=np.int64)
+    lc = lp.copy()
+    for n in (1, 9, 16, 20):
+        new = rng.standard_normal((B, H, n, D))
+        orc.kv_append_paged(pages, table, lp, new)
+        orc.kv_append(contig, lc, new)
+    assert np.array_equal(lp, lc)
+    assert np.array_equal(orc.gather_pages(pages, table, lp, max_len=max_pages * ps), np.where(
+        np.arange(max_pages * ps)[None, None, :, None] < lc[:, None, None, None], contig, 0.0))
