@@ -4,8 +4,9 @@
 Step = one causal GQA prefill forward with LSE on the Llama-3-8B attention shape (B=4, Hq=32, Hkv=8,
 S=2048, D=128, bf16), inputs resident in HBM.  ``value`` is algorithmic TFLOP/s (visible pairs only:
 4*B*Hq*D*S(S+1)/2) over the timed steps.  Also reported, each on its own synthetic inputs: split-KV
-decode HBM GB/s (B=64, Hq=32, Hkv=8, D=128, lengths U[512, 8192]), the ring step (4 blocks + LSE
-merge), MMDiT joint attention in bf16 and fp8, and the fp32-spec causal MHA case.  The CPU baseline is
+decode HBM GB/s (B=64, Hq=32, Hkv=8, D=128, lengths U[512, 8192]) with a contiguous and a paged cache,
+one decode step (KV-cache append of one token + decode), the ring step (4 blocks + LSE merge), MMDiT
+joint attention in bf16 and fp8, and the fp32-spec causal MHA case.  The CPU baseline is
 libtorch's CPU SDPA in bf16 (the call SdpaOp::Compute makes on a CPU mesh) on the same prefill, timed
 on this host over about ten seconds of repetitions, and compared with the GPU output.
 
@@ -134,6 +135,26 @@ def secondary_workloads(torch, F, dev, timer):
                            "note": "L2/MALL flushed before every rep"}
     log(f"decode B=64 Hq=32 Hkv=8 lengths U[512,8192]: {med * 1e6:.1f} us, {gbs:.0f} GB/s "
         f"({100 * gbs * 1e9 / PEAK_HBM:.1f}% of HBM)")
+
+    # one decode step: append the new token's K/V (written at position L - 1 of each sequence, so the
+    # attended length stays the bench's), then decode; lengths are reset outside the timed region
+    base = (lens - 1).to(torch.int32)
+    lens_run = base.clone()
+    k1 = torch.randn(Bd, 1, Hkvd, Dd, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+    v1 = torch.randn(Bd, 1, Hkvd, Dd, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+
+    def step():
+        F.kv_cache_append(kc, vc, lens_run, k1, v1)
+        F.decode_attention(qd, kc, vc, lens_run)
+
+    def reset():
+        flush()
+        lens_run.copy_(base)
+
+    med_s, _ = timer.run(step, reps=20, flush=reset)
+    extras["decode_step_c3"] = {"us": round(med_s * 1e6, 1), "GB/s": round(dbytes / med_s / 1e9, 1),
+                                "note": "kv_cache_append of 1 token per sequence + decode_attention"}
+    log(f"decode step (append 1 token + decode): {med_s * 1e6:.1f} us")
 
     # the same caches in 16-token pages [P, Hkv, 16, D], scattered over the pool by a random block table
     ps = 16
