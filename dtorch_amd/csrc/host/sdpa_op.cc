@@ -9,6 +9,7 @@
 #include <c10/hip/HIPStream.h>
 
 #include <cmath>
+#include <limits>
 #include <sstream>
 #include <stdexcept>
 
@@ -99,8 +100,53 @@ struct PrefillResult {
     at::Tensor o, lse;
 };
 
+// attn_mask -> the additive fp32 form the kernels read: [B, Hq, Sq, Sk] with broadcast axes at stride 0,
+// key stride 1, other strides multiples of 4 and a 16-byte aligned base.  A boolean mask keeps True
+// entries (0) and hides False ones (-inf), as torch::scaled_dot_product_attention does.  Only the
+// mask's own (unbroadcast) extent is ever copied: to fp32, and to a row pitch padded to 4 when needed.
+at::Tensor PrepareMask(const at::Tensor& m, const at::Tensor& q, const at::Tensor& k, int64_t B, int64_t Hq,
+                       int64_t Sq, int64_t Sk) {
+    if (m.device() != q.device()) Throw("attn_mask must be on the query's device");
+    if (m.scalar_type() != at::kBool && !at::isFloatingType(m.scalar_type()))
+        Throw("attn_mask must be boolean or floating point");
+    if (m.dim() < 1) Throw("attn_mask must have at least one dimension");
+    at::Tensor mf = m.scalar_type() == at::kBool
+                        ? at::where(m, at::zeros({}, q.options().dtype(at::kFloat)),
+                                    at::full({}, -std::numeric_limits<float>::infinity(), q.options().dtype(at::kFloat)))
+                        : m.to(at::kFloat);
+    if (mf.size(-1) == 1 && Sk > 1) {  // broadcast along the keys: spell it out (the kernel reads key stride 1)
+        std::vector<int64_t> sz = mf.sizes().vec();
+        sz.back() = Sk;
+        mf = mf.expand(sz);
+    }
+    bool ok = mf.stride(-1) == 1 && (reinterpret_cast<uintptr_t>(mf.data_ptr()) & 15u) == 0;
+    for (int64_t i = 0; i + 1 < mf.dim(); ++i)
+        if (mf.size(i) > 1 && mf.stride(i) % 4 != 0) ok = false;
+    if (!ok) {  // padded row pitch, contiguous otherwise
+        std::vector<int64_t> sz = mf.sizes().vec();
+        const int64_t n = sz.back();
+        sz.back() = (n + 3) / 4 * 4;
+        at::Tensor pad = at::zeros(sz, mf.options());
+        pad.narrow(-1, 0, n).copy_(mf);
+        mf = pad.narrow(-1, 0, n);
+    }
+    std::vector<int64_t> full = q.sizes().vec();
+    full.back() = k.size(-2);
+    at::Tensor e;
+    try {
+        e = mf.expand(full);
+    } catch (const c10::Error&) {
+        Throw("attn_mask is not broadcastable to [..., Hq, L, S]");
+    }
+    if (e.dim() > 4) e = e.reshape({B, Hq, Sq, Sk});  // a view when the batch axes fold, else a copy
+    if (e.stride(3) != 1 && Sk > 1) Throw("internal: mask key stride");
+    for (int i = 0; i < 3; ++i)
+        if (e.size(i) > 1 && e.stride(i) % 4 != 0) e = e.contiguous();  // only after a reshape copy of odd pitch
+    return e;
+}
+
 PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_, const SdpaParam& prm,
-                         int64_t qOffset, int64_t kOffset, bool wantLse) {
+                         int64_t qOffset, int64_t kOffset, bool wantLse, const at::Tensor* mask = nullptr) {
     CheckDevice({&q_, &k_, &v_});
     c10::DeviceGuard guard(q_.device());
     if (q_.dim() != k_.dim() || q_.dim() != v_.dim()) Throw("query, key and value must have the same rank");
@@ -153,6 +199,13 @@ PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::T
     a.scale = prm.scale.has_value() ? (float)prm.scale.value() : 0.f;
     a.causal = prm.isCausal ? 1 : 0;
     a.q_offset = qOffset, a.k_offset = kOffset;
+    at::Tensor maskf;
+    if (mask != nullptr) {
+        if (fp8) Throw("attn_mask is not supported with sage_attn_type 'native_fp8'");
+        maskf = PrepareMask(*mask, q_, k_, q.B, q.H, q.S, k.S);
+        a.mask = maskf.data_ptr<float>();
+        for (int i = 0; i < 3; ++i) a.mask_stride[i] = maskf.size(i) > 1 ? maskf.stride(i) : 0;
+    }
 
     at::Tensor q8, k8, v8, qd, kd, vd;
     if (fp8) {
@@ -257,18 +310,16 @@ void SdpaOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& output
     if (inputs.size() != 4) Throw("SdpaOp expects 4 inputs {query, key, value, attn_mask}");
     if (!inputs[0].has_value() || !inputs[1].has_value() || !inputs[2].has_value())
         Throw("query, key and value are required");
-    if (inputs[3].has_value() && inputs[3]->defined())
-        Throw("attn_mask is not supported by the MI355X kernels (use is_causal)");
-    outputs.push_back(RunPrefill(*inputs[0], *inputs[1], *inputs[2], mParam, 0, 0, false).o);
+    const at::Tensor* mask = inputs[3].has_value() && inputs[3]->defined() ? &*inputs[3] : nullptr;
+    outputs.push_back(RunPrefill(*inputs[0], *inputs[1], *inputs[2], mParam, 0, 0, false, mask).o);
 }
 
 void SdpaWithLseOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {
     if (inputs.size() != 4) Throw("SdpaWithLseOp expects 4 inputs {query, key, value, attn_mask}");
     if (!inputs[0].has_value() || !inputs[1].has_value() || !inputs[2].has_value())
         Throw("query, key and value are required");
-    if (inputs[3].has_value() && inputs[3]->defined())
-        Throw("attn_mask is not supported by the MI355X kernels (use is_causal)");
-    PrefillResult r = RunPrefill(*inputs[0], *inputs[1], *inputs[2], mParam, mQOffset, mKOffset, true);
+    const at::Tensor* mask = inputs[3].has_value() && inputs[3]->defined() ? &*inputs[3] : nullptr;
+    PrefillResult r = RunPrefill(*inputs[0], *inputs[1], *inputs[2], mParam, mQOffset, mKOffset, true, mask);
     outputs.push_back(r.o);
     outputs.push_back(r.lse);
 }

@@ -47,6 +47,12 @@ struct PrefillParams {
     int32_t delta;  // key j visible to query i iff j <= i + delta (causal only)
     float c;        // softmax scale * log2(e)
     int32_t xcd_map;  // 1: group the workgroups of each (batch, kv head) slice on one XCD
+    // additive fp32 attention mask (MASKED kernels): element (b, h, i, j) at
+    // mask + b*ms_b + h*ms_h + i*ms_l + j (key stride 1, strides multiples of 4, 16-byte aligned base);
+    // it enters the raw scores as m / scale, so -inf and the dtype-minimum fills both hide a key
+    const float* mask;
+    int64_t ms_b, ms_h, ms_l;
+    float inv_scale;
 };
 
 template <bool CAUSAL>
@@ -68,7 +74,7 @@ __device__ __forceinline__ int kswz(int r) {
     return D >= 128 ? 4 * (r & 3) + ((r >> 2) & 3) : 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
 }
 
-template <typename T, int D, int QT, bool CAUSAL>
+template <typename T, int D, int QT, bool CAUSAL, bool MASKED>
 __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams p) {
     constexpr int NW = 4;
     constexpr int BN = 64;
@@ -164,17 +170,38 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     const int tr_d = 16 * (blk & 1) + 4 * (bl & 3);  // D0 offset within the 32-d tile + 4a
     const int tr_k4 = 4 * (blk >> 1);           // 4 * hf
 
+    // MASKED: the mask slab of (b, hq) behind a buffer resource, so reads past its last row return 0
+    // (those keys are hidden by the ragged-tail mask anyway).  Lane (l32, hf) reads, for query row
+    // wq0 + l32, the four consecutive keys of each of its 4 groups per 32-key tile.
+    const float* mbase_p = MASKED ? p.mask + b * p.ms_b + hq * p.ms_h : nullptr;
+    const auto mrs = make_rsrc(mbase_p, MASKED ? (uint32_t)((((int64_t)(p.Sq - 1) * p.ms_l + p.Sk) * 4)) : 0u);
+    const uint32_t mrow_off = MASKED ? (uint32_t)((int64_t)min(wq0 + l32, p.Sq - 1) * p.ms_l * 4) : 0u;
+
     // One key tile.  Kc/Vc hold tile t; Kn/Vn receive tile t+1.
     auto tile = [&](const T* Kc, const T* Vc, T* Kn, T* Vn, int t) {
         wait_vmem();
         lds_barrier();  // tile t landed everywhere; every wave finished tile t-1 (so Kn/Vn are free)
-        if (t + 1 < nt) {
-            dma(Kn, kp, krow, p.ks_s, t + 1);
-            dma(Vn, vp, vrow, p.vs_s, t + 1);
-        }
+        // Unmasked: the next tile's loads go out first.  Masked: after this tile's mask values have been
+        // waited for (the compiler's wait for them would otherwise also wait for the tile loads).
+        auto next_tile = [&]() {
+            if (t + 1 < nt) {
+                dma(Kn, kp, krow, p.ks_s, t + 1);
+                dma(Vn, vp, vrow, p.vs_s, t + 1);
+            }
+        };
+        if constexpr (!MASKED) next_tile();
         const int kbase = t * BN;
-        if (CAUSAL && kbase > wq0 + 31 + p.delta) return;  // every row of this wave precedes the tile
+        if (CAUSAL && kbase > wq0 + 31 + p.delta) {  // every row of this wave precedes the tile
+            if constexpr (MASKED) next_tile();
+            return;
+        }
         const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && (kbase + BN - 1 > wq0 + p.delta));
+        u32x4 mraw[KT * 4];
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int g = 0; g < KT * 4; ++g)  // keys kbase + 32*(g/4) + 8*(g%4) + 4*hf .. +3
+                mraw[g] = buf_ld16(mrs, mrow_off + (uint32_t)((kbase + 32 * (g >> 2) + 8 * (g & 3) + 4 * hf) * 4));
+        }
 
         f32x16 s[KT];
 #pragma unroll
@@ -200,6 +227,17 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int g = 0; g < KT * 4; ++g) {
+                const f32x4 m = __builtin_bit_cast(f32x4, mraw[g]);
+                s[g >> 2][4 * (g & 3) + 0] += m.x * p.inv_scale;
+                s[g >> 2][4 * (g & 3) + 1] += m.y * p.inv_scale;
+                s[g >> 2][4 * (g & 3) + 2] += m.z * p.inv_scale;
+                s[g >> 2][4 * (g & 3) + 3] += m.w * p.inv_scale;
+            }
+            next_tile();
+        }
         if (need_mask) {
             // Element i of key tile kt holds key kbase + kt*32 + 8*(i/4) + 4*hf + i%4; it is visible
             // iff its compile-time offset kt*32 + 8*(i/4) + i%4 is <= lim.
@@ -336,7 +374,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
 
 // ------------------------------------------------------------------------------------------------
 
-template <typename T, int D, int QT, bool CAUSAL>
+template <typename T, int D, int QT, bool CAUSAL, bool MASKED>
 static int launch_prefill(const PrefillParams& prm, hipStream_t stream) {
     constexpr int BM = 4 * QT * 32;
     PrefillParams p = prm;
@@ -344,19 +382,27 @@ static int launch_prefill(const PrefillParams& prm, hipStream_t stream) {
     const int64_t grid = (int64_t)p.n_qblocks * p.B * p.Hq;
     if (grid == 0) return DTATTN_OK;
     if (grid > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill grid too large (%lld blocks)", (long long)grid);
-    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, QT, CAUSAL>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, QT, CAUSAL, MASKED>), dim3((unsigned)grid), dim3(256), 0, stream, p);
     return check_launch("prefill_fwd_kernel");
+}
+
+template <typename T, bool MASKED>
+static int dispatch_prefill_m(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
+    if (D == 128) {
+        return causal ? launch_prefill<T, 128, 1, true, MASKED>(p, stream)
+                      : launch_prefill<T, 128, 1, false, MASKED>(p, stream);
+    }
+    if (D == 64) {
+        return causal ? launch_prefill<T, 64, 1, true, MASKED>(p, stream)
+                      : launch_prefill<T, 64, 1, false, MASKED>(p, stream);
+    }
+    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %d not supported (64 or 128)", D);
 }
 
 template <typename T>
 static int dispatch_prefill(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
-    if (D == 128) {
-        return causal ? launch_prefill<T, 128, 1, true>(p, stream) : launch_prefill<T, 128, 1, false>(p, stream);
-    }
-    if (D == 64) {
-        return causal ? launch_prefill<T, 64, 1, true>(p, stream) : launch_prefill<T, 64, 1, false>(p, stream);
-    }
-    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %d not supported (64 or 128)", D);
+    return p.mask != nullptr ? dispatch_prefill_m<T, true>(p, D, causal, stream)
+                             : dispatch_prefill_m<T, false>(p, D, causal, stream);
 }
 
 int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_t stream);
@@ -408,6 +454,19 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     if (delta64 < -lim) delta64 = -lim;
     const int32_t delta = (int32_t)delta64;
 
+    if (a->mask != nullptr) {
+        if (a->dtype == DTATTN_FP8_E4M3FN)
+            return fail(DTATTN_ERR_UNSUPPORTED, "prefill: an attention mask is not supported with fp8 inputs");
+        for (int j = 0; j < 3; ++j)
+            if (a->mask_stride[j] < 0 || a->mask_stride[j] % 4 != 0)
+                return fail(DTATTN_ERR_UNSUPPORTED, "prefill: mask stride[%d]=%lld must be a non-negative multiple of 4",
+                            j, (long long)a->mask_stride[j]);
+        if ((reinterpret_cast<uintptr_t>(a->mask) & 15u) != 0)
+            return fail(DTATTN_ERR_UNSUPPORTED, "prefill: mask must be 16-byte aligned");
+        // one (b, h) slab of the mask is addressed with 32-bit byte offsets
+        if (((a->Sq - 1) * a->mask_stride[2] + a->Sk + 64) * 4 >= ((int64_t)1 << 32))
+            return fail(DTATTN_ERR_UNSUPPORTED, "prefill: mask slab of one (batch, head) exceeds 4 GB");
+    }
     if (a->dtype == DTATTN_FP8_E4M3FN) {
         if (a->o_dtype != DTATTN_BF16) return fail(DTATTN_ERR_UNSUPPORTED, "prefill fp8: output must be bf16");
         if (a->q_descale == nullptr || a->k_descale == nullptr || a->v_descale == nullptr)
@@ -440,6 +499,9 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     p.delta = delta;
     p.c = c;
     p.xcd_map = (p.B * p.Hkv) % 8 == 0 ? 1 : 0;
+    p.mask = a->mask;
+    p.ms_b = a->mask_stride[0], p.ms_h = a->mask_stride[1], p.ms_l = a->mask_stride[2];
+    p.inv_scale = 1.0f / scale;
     const int D = (int)a->D;
     const bool causal = a->causal != 0;
     if (a->dtype == DTATTN_BF16) return dispatch_prefill<bf16_t>(p, D, causal, stream);

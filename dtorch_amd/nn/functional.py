@@ -79,7 +79,9 @@ def scaled_dot_product_attention(
     """O = softmax(scale Q K^T [causal, top-left]) V on the gfx950 kernels.
 
     ``dropout_p`` is accepted and ignored, as in the reference (neural_network.cc:147-154 drops it and
-    SdpaOp::Compute passes 0.0).  ``attn_mask`` other than None is rejected by the host operator.
+    SdpaOp::Compute passes 0.0).  ``attn_mask`` follows torch: broadcastable to [..., Hq, L, S], boolean
+    (True keeps a key) or floating point (added to the scaled logits), applied together with ``is_causal``;
+    not supported with ``native_fp8``.
     """
     _check_option(query, sdpa_option)
     op = _h.SdpaOp(_param(is_causal, scale, enable_gqa, sdpa_option))
@@ -96,11 +98,13 @@ def scaled_dot_product_attention_with_lse(
     q_offset: int = 0,
     k_offset: int = 0,
     sdpa_option: SdpaOption = SdpaOption(),
+    attn_mask: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(O, LSE[..., Hq, L] fp32).  Causal rule: key j visible to query i iff j + k_offset <= i + q_offset."""
+    """(O, LSE[..., Hq, L] fp32).  Causal rule: key j visible to query i iff j + k_offset <= i + q_offset.
+    ``attn_mask`` as in scaled_dot_product_attention, applied together with the causal rule."""
     _check_option(query, sdpa_option)
     op = _h.SdpaWithLseOp(_param(is_causal, scale, enable_gqa, sdpa_option), int(q_offset), int(k_offset))
-    o, lse = op.compute([query, key, value, None])
+    o, lse = op.compute([query, key, value, attn_mask])
     return o, lse
 
 

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define DTATTN_ABI_VERSION 3
+#define DTATTN_ABI_VERSION 4
 
 typedef enum {
     DTATTN_OK = 0,
@@ -45,7 +45,7 @@ typedef enum {
  * Replaces the arithmetic of SdpaOp::Compute, i.e. the libtorch call at
  * dtorch/core/operators/standard/scaled_dot_product_attention_op.cc:107-109
  * (torch::scaled_dot_product_attention(q, k, v, mask, 0.0, isCausal, scale, enableGqa)), for
- * mask == nullopt.  GQA: query head h reads kv head h / (Hq / Hkv) (the op's enableGqa and the
+ * mask == nullopt or an additive mask (below).  GQA: query head h reads kv head h / (Hq / Hkv) (the op's enableGqa and the
  * Llama port's repeat_kv, python/dtorch/test/modules/llama.py:80-85).  Causal rule: key j is
  * visible to query i iff j + k_offset <= i + q_offset; (0, 0) is torch's top-left alignment, a ring
  * block uses the chunks' global offsets.  Rows that see no key get O = 0 and LSE = -inf.
@@ -73,6 +73,14 @@ typedef struct {
     const float* q_descale; /* FP8 only: [B, Hq] fp32, real = code * descale */
     const float* k_descale; /* FP8 only: [B, Hkv] */
     const float* v_descale; /* FP8 only: [B, Hkv] */
+    /* Optional additive attention mask (BF16/FP16 only; NULL: none), the attn_mask of
+     * scaled_dot_product_attention_op.cc:107-109 in float form: logits = scale * q.k + m, applied together
+     * with the causal rule.  Element (b, h, i, j) is mask[b*mask_stride[0] + h*mask_stride[1] +
+     * i*mask_stride[2] + j] (key stride 1; a stride of 0 broadcasts); strides are multiples of 4 and the
+     * pointer is 16-byte aligned.  -inf, or any value whose m / scale overflows fp32 (the dtype-minimum
+     * fill of additive masks), hides the key; a boolean mask is passed as 0 / -inf. */
+    const float* mask;
+    int64_t mask_stride[3];
 } dtattn_prefill_args;
 
 int dtattn_prefill_fwd(const dtattn_prefill_args* args, void* stream);

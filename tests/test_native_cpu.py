@@ -59,7 +59,8 @@ class PrefillArgs(ctypes.Structure):
                 ("o_stride", ctypes.c_int64 * 3), ("lse_stride", ctypes.c_int64 * 2),
                 ("dtype", ctypes.c_int32), ("o_dtype", ctypes.c_int32), ("scale", ctypes.c_float),
                 ("causal", ctypes.c_int32), ("q_offset", ctypes.c_int64), ("k_offset", ctypes.c_int64),
-                ("q_descale", ctypes.c_void_p), ("k_descale", ctypes.c_void_p), ("v_descale", ctypes.c_void_p)]
+                ("q_descale", ctypes.c_void_p), ("k_descale", ctypes.c_void_p), ("v_descale", ctypes.c_void_p),
+                ("mask", ctypes.c_void_p), ("mask_stride", ctypes.c_int64 * 3)]
 
 
 def _args(**kw):
@@ -94,6 +95,19 @@ def test_prefill_validation(kw, code, text):
     a = _args(**kw)
     assert lib.dtattn_prefill_fwd(ctypes.byref(a), None) == code
     assert text in _last_error()
+
+
+def test_prefill_mask_validation():
+    # every case fails validation before any launch (the pointers are never dereferenced)
+    lib.dtattn_prefill_fwd.restype = ctypes.c_int
+    a = _args(mask=0x20000)
+    a.mask_stride[0], a.mask_stride[1], a.mask_stride[2] = 0, 0, 6  # key-row pitch not a multiple of 4
+    assert lib.dtattn_prefill_fwd(ctypes.byref(a), None) == 2 and "mask stride" in _last_error()
+    a.mask_stride[2] = 64
+    a.mask = 0x20004  # not 16-byte aligned
+    assert lib.dtattn_prefill_fwd(ctypes.byref(a), None) == 2 and "aligned" in _last_error()
+    a.mask, a.dtype = 0x20000, 2
+    assert lib.dtattn_prefill_fwd(ctypes.byref(a), None) == 2 and "fp8" in _last_error()
 
 
 def test_prefill_null_args():

@@ -360,3 +360,20 @@ def test_kv_append_paged_matches_contiguous():
     assert np.array_equal(lp, lc)
     assert np.array_equal(orc.gather_pages(pages, table, lp, max_len=max_pages * ps), np.where(
         np.arange(max_pages * ps)[None, None, :, None] < lc[:, None, None, None], contig, 0.0))
+
+
+def test_masks_match_libtorch():
+    # boolean and additive masks, broadcast from several shapes, with and without is_causal
+    rng = np.random.default_rng(33)
+    B, H, L, S, D = 2, 3, 11, 17, 16
+    q, k, v = (rng.standard_normal((B, H, n, D), dtype=np.float32) for n in (L, S, S))
+    keep = rng.random((L, S)) < 0.6
+    keep[:, 0] = True  # every row keeps a key (torch zeroes fully hidden rows; covered elsewhere)
+    fmask = np.where(rng.random((B, 1, L, S)) < 0.3, np.finfo(np.float32).min, rng.standard_normal((B, 1, L, S)))
+    fmask[..., 0] = 0.0
+    fmask = fmask.astype(np.float32)
+    for mask, causal in ((keep, False), (keep, True), (fmask, False), (fmask, True), (fmask[:, :, :1], False)):
+        o, lse = orc.sdpa_fwd(q, k, v, attn_mask=mask, is_causal=causal)
+        tm = torch.from_numpy(np.ascontiguousarray(mask))
+        ref = cpu.sdpa(_t(q), _t(k), _t(v), attn_mask=tm, is_causal=causal).double().numpy()
+        assert np.max(np.abs(o - ref)) < 2e-5, (mask.dtype, mask.shape, causal)
