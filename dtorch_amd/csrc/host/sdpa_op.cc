@@ -172,8 +172,8 @@ PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::T
 
     const c10::ScalarType st = q_.scalar_type();
     if (k_.scalar_type() != st || v_.scalar_type() != st) Throw("query, key and value dtypes differ");
-    if (st != c10::ScalarType::BFloat16 && st != c10::ScalarType::Half)
-        Throw(std::string("dtype ") + c10::toString(st) + " is not supported by the MI355X kernels (bf16, fp16)");
+    if (st != c10::ScalarType::BFloat16 && st != c10::ScalarType::Half && st != c10::ScalarType::Float)
+        Throw(std::string("dtype ") + c10::toString(st) + " is not supported by the MI355X kernels (bf16, fp16, fp32)");
     if (fp8 && st != c10::ScalarType::BFloat16) Throw("native_fp8 takes bf16 inputs");
 
     std::vector<int64_t> oshape = q_.sizes().vec();

@@ -1,0 +1,289 @@
+// fp32 attention forward for gfx950 on the fp32 matrix cores (v_mfma_f32_32x32x2_f32), with per-row
+// LSE.
+//
+// This is the fp32 branch of SdpaOp::Compute: the libtorch call at
+// dtorch/core/operators/standard/scaled_dot_product_attention_op.cc:107-109 computes fp32 inputs in
+// fp32, and DTorch's own Llama test (python/dtorch/test/modules/test_llama.py:26-64) runs the model
+// in fp32 on the GPU at a 1e-4 tolerance.  Q K^T, the softmax, P and P V therefore all stay in fp32
+// here; nothing is rounded to a 16-bit type.
+//
+// Work decomposition and layout follow the bf16 kernel (prefill_fwd.hip): a workgroup is 4 waves of
+// 32 query rows of one (batch, query head); Q fragments stay in registers; S^T = K Q^T and
+// O^T = V^T P^T, so each lane owns one query column and the per-query softmax state is a per-lane
+// scalar.  What differs:
+//   - Key tiles of 32 rows (an fp32 row is twice the bytes): K and V tiles [32][D] fp32,
+//     double-buffered, 64 KB per workgroup at D = 128, two workgroups per CU.
+//   - The MFMA reduction index is 2 wide.  In S^T step s, lane half h contributes dimension
+//     d = (D/2) h + s, so a lane's Q fragment and its K reads are contiguous runs of D/2 floats.
+//     Row i of the d-block `blk` of O^T is dimension d = DT i + blk (DT = D / 32), so one LDS read of
+//     DT consecutive floats of a V row feeds the DT MFMAs of a PV step.
+//   - LDS rows keep 16-byte chunk c at c ^ (r & 15): a 16-lane group of K reads (16 rows, one chunk
+//     each) and of V reads (one row, 16 consecutive chunks) touches 16 distinct bank groups.
+//
+// Pipeline per key tile j (one barrier per tile), as in the bf16 kernel:
+//   wait own loads + barrier | K[j+1], V[j+1] -> LDS (async) | S^T = K[j] Q^T | softmax |
+//   O^T += V^T(j) P^T(j)
+#include "dtattn_common.hpp"
+#include "prefill_params.hpp"
+
+namespace dtattn {
+
+template <int D, bool CAUSAL, bool MASKED>
+__global__ void __launch_bounds__(256, 2) prefill_f32_kernel(const PrefillParams p) {
+    constexpr int NW = 4;
+    constexpr int BN = 32;           // keys per tile
+    constexpr int BM = NW * 32;      // query rows per workgroup
+    constexpr int DCH = D / 4;       // 16-byte chunks per row
+    constexpr int HD = D / 2;        // S^T k-steps: dimensions per lane half
+    constexpr int DT = D / 32;       // 32-row d blocks of O^T
+    static_assert(D == 64 || D == 128, "head dim 64 or 128");
+    typedef float fvec __attribute__((ext_vector_type(DT)));
+
+    __shared__ __attribute__((aligned(16))) float Ka[BN * D];
+    __shared__ __attribute__((aligned(16))) float Kb[BN * D];
+    __shared__ __attribute__((aligned(16))) float Va[BN * D];
+    __shared__ __attribute__((aligned(16))) float Vb[BN * D];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31;
+    const int hf = lane >> 5;
+
+    const BlockCoord bc = block_coord<CAUSAL>(p);
+    const int qb = bc.qb, b = bc.b, hq = bc.hq, hk = bc.hk;
+
+    const float* qp = reinterpret_cast<const float*>(p.q) + b * p.qs_b + hq * p.qs_h;
+    const float* kp = reinterpret_cast<const float*>(p.k) + b * p.ks_b + hk * p.ks_h;
+    const float* vp = reinterpret_cast<const float*>(p.v) + b * p.vs_b + hk * p.vs_h;
+
+    const int q0 = qb * BM;
+    const int wq0 = q0 + wave * 32;
+
+    int kend = p.Sk;
+    if (CAUSAL) {
+        const int lim = q0 + BM + p.delta;  // keys < lim can be visible
+        kend = lim < 0 ? 0 : (lim < p.Sk ? lim : p.Sk);
+    }
+    const int nt = (kend + BN - 1) / BN;
+
+    // Q fragment (B operand of S^T = K Q^T): lane (l32, hf) holds Q[wq0 + l32][HD*hf + s], s < HD.
+    float qf[HD];
+    {
+        const int qrow = wq0 + l32;
+#pragma unroll
+        for (int g = 0; g < HD / 4; ++g) {
+            u32x4 raw = {0u, 0u, 0u, 0u};
+            if (qrow < p.Sq) raw = ld16(qp + (int64_t)qrow * p.qs_s + HD * hf + 4 * g);
+            const f32x4 x = __builtin_bit_cast(f32x4, raw);
+            qf[4 * g + 0] = x.x, qf[4 * g + 1] = x.y, qf[4 * g + 2] = x.z, qf[4 * g + 3] = x.w;
+        }
+    }
+
+    f32x16 oacc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[dt][i] = 0.f;
+    float mrow = kNegInf, lrow = 0.f;
+
+    const int krow = (int)(p.ks_s * (int64_t)sizeof(float));  // row pitch in bytes (host-checked)
+    const int vrow = (int)(p.vs_s * (int64_t)sizeof(float));
+
+    // Tile t -> LDS by direct buffer->LDS loads: one wave instruction fills 1 KB (lane l -> byte 16*l),
+    // i.e. 1024 / (4 D) rows; lane l loads the global chunk that belongs at its LDS slot,
+    // c = slot ^ (row & 15).  The buffer resource covers the tile's valid rows; rows past Sk read zeros.
+    auto dma = [&](float* dst, const float* base, int pitch, int64_t stride, int t) {
+        constexpr int ROWS_PER_INSTR = 1024 / (4 * D);
+        constexpr int INSTR = BN / ROWS_PER_INSTR / NW;  // per wave
+        const int rows = min(BN, p.Sk - t * BN);
+        const auto rs = make_rsrc(base + (int64_t)t * BN * stride, (uint32_t)((rows - 1) * pitch + D * 4));
+#pragma unroll
+        for (int i = 0; i < INSTR; ++i) {
+            const int r0 = (wave * INSTR + i) * ROWS_PER_INSTR;
+            const int r = r0 + lane / DCH;
+            const int c = (lane % DCH) ^ (r & 15);
+            buf_ld16_lds_async(rs, dst + r0 * D, (uint32_t)(r * pitch + c * 16));
+        }
+    };
+
+    // MASKED: lane (l32, hf) reads, for query row wq0 + l32, keys kbase + 8g + 4hf .. +3 (g < 4) of
+    // the (b, hq) mask slab, behind a buffer resource (reads past its last row return 0; those keys
+    // are hidden by the ragged-tail mask anyway).
+    const float* mbase_p = MASKED ? p.mask + b * p.ms_b + hq * p.ms_h : nullptr;
+    const auto mrs = make_rsrc(mbase_p, MASKED ? (uint32_t)((((int64_t)(p.Sq - 1) * p.ms_l + p.Sk) * 4)) : 0u);
+    const uint32_t mrow_off = MASKED ? (uint32_t)((int64_t)min(wq0 + l32, p.Sq - 1) * p.ms_l * 4) : 0u;
+
+    auto tile = [&](const float* Kc, const float* Vc, float* Kn, float* Vn, int t) {
+        wait_vmem();
+        lds_barrier();  // tile t landed everywhere; every wave finished tile t-1 (so Kn/Vn are free)
+        auto next_tile = [&]() {
+            if (t + 1 < nt) {
+                dma(Kn, kp, krow, p.ks_s, t + 1);
+                dma(Vn, vp, vrow, p.vs_s, t + 1);
+            }
+        };
+        if constexpr (!MASKED) next_tile();
+        const int kbase = t * BN;
+        if (CAUSAL && kbase > wq0 + 31 + p.delta) {  // every row of this wave precedes the tile
+            if constexpr (MASKED) next_tile();
+            return;
+        }
+        const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && (kbase + BN - 1 > wq0 + p.delta));
+        u32x4 mraw[4];
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) mraw[g] = buf_ld16(mrs, mrow_off + (uint32_t)((kbase + 8 * g + 4 * hf) * 4));
+        }
+
+        // S^T = K Q^T: lane (l32, hf) supplies K[kbase + l32][HD*hf + s] at step s.
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = 0.f;
+        {
+            const int r = l32;
+#pragma unroll
+            for (int g = 0; g < HD / 4; ++g) {
+                const int c = (HD / 4) * hf + g;
+                const f32x4 kv = *reinterpret_cast<const f32x4*>(Kc + r * D + 4 * (c ^ (r & 15)));
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * g + 0], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * g + 1], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * g + 2], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * g + 3], s, 0, 0, 0);
+            }
+            // K reads run two groups of four MFMAs ahead of their use (hoisting them all would cost
+            // 4 D registers)
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int g = 0; g < HD / 4 - 2; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        }
+        // Element i of s holds key kbase + 8*(i/4) + 4*hf + i%4 of query wq0 + l32.
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 m = __builtin_bit_cast(f32x4, mraw[g]);
+                s[4 * g + 0] += m.x * p.inv_scale;
+                s[4 * g + 1] += m.y * p.inv_scale;
+                s[4 * g + 2] += m.z * p.inv_scale;
+                s[4 * g + 3] += m.w * p.inv_scale;
+            }
+            next_tile();
+        }
+        if (need_mask) {
+            int lim = p.Sk - 1 - kbase;
+            if (CAUSAL) lim = min(lim, wq0 + l32 + p.delta - kbase);
+            lim -= 4 * hf;
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (8 * (i >> 2) + (i & 3) > lim) s[i] = kNegInf;
+        }
+        float mx = kNegInf;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+        mx = max_xor32(mx);
+        const float mcand = fmaxf(mrow, mx * p.c);
+        if (__any(mcand - mrow > kRescaleThreshold)) {  // wave-uniform
+            const float alpha = fast_exp2(mrow - (mcand == kNegInf ? 0.f : mcand));
+            mrow = mcand;
+            lrow *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+        }
+        const float mbase = (mrow == kNegInf) ? 0.f : mrow;
+        float pr[16];
+        float ls = lrow;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            pr[i] = fast_exp2(__builtin_fmaf(s[i], p.c, -mbase));
+            ls += pr[i];
+        }
+        lrow = ls;
+
+        // O^T += V^T P^T over 16 steps: step (jj, rr) pairs key 8jj + rr (lane half 0) with key
+        // 8jj + 4 + rr (half 1), the keys of the lane's own score element 4jj + rr.
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int key = 8 * jj + 4 * hf + rr;
+                const int e = DT * l32;  // first of the DT consecutive floats this lane reads
+                const fvec vv = *reinterpret_cast<const fvec*>(Vc + key * D + 4 * ((e >> 2) ^ (key & 15)) + (e & 3));
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[dt], pr[4 * jj + rr], oacc[dt], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+        for (int i = 0; i < 14; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, DT, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * DT, 0);
+    };
+
+    if (nt > 0) {
+        dma(Ka, kp, krow, p.ks_s, 0);
+        dma(Va, vp, vrow, p.vs_s, 0);
+    }
+    // Q fragments (and tile 0) complete here, visibly to the compiler, so that it inserts no load
+    // waits inside the loop (where they would also drain the asynchronous tile loads).
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    for (int t = 0; t < nt; t += 2) {  // unrolled by two so each tile names its buffers statically
+        tile(Ka, Va, Kb, Vb, t);
+        if (t + 1 < nt) tile(Kb, Vb, Ka, Va, t + 1);
+    }
+
+    // Epilogue: element i of O^T block dt is O[wq0 + l32][DT * (8*(i/4) + 4*hf + i%4) + dt], so the
+    // DT blocks of one element index form DT consecutive floats of the output row.
+    const float l = sum_xor32(lrow);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int qrow = wq0 + l32;
+    if (qrow < p.Sq) {
+        float* orow = reinterpret_cast<float*>(p.o) + b * p.os_b + hq * p.os_h + (int64_t)qrow * p.os_s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            fvec o;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] = oacc[dt][i] * inv;
+            *reinterpret_cast<fvec*>(orow + DT * (8 * (i >> 2) + 4 * hf + (i & 3))) = o;
+        }
+        if (p.lse != nullptr && hf == 0)
+            p.lse[b * p.lses_b + hq * p.lses_h + qrow] = l > 0.f ? (mrow + __log2f(l)) * kLn2 : kNegInf;
+    }
+}
+
+template <int D, bool CAUSAL, bool MASKED>
+static int launch_prefill_f32(const PrefillParams& prm, hipStream_t stream) {
+    constexpr int BM = 4 * 32;
+    PrefillParams p = prm;
+    p.n_qblocks = (p.Sq + BM - 1) / BM;
+    const int64_t grid = (int64_t)p.n_qblocks * p.B * p.Hq;
+    if (grid == 0) return DTATTN_OK;
+    if (grid > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill grid too large (%lld blocks)", (long long)grid);
+    hipLaunchKernelGGL((prefill_f32_kernel<D, CAUSAL, MASKED>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    return check_launch("prefill_f32_kernel");
+}
+
+template <bool MASKED>
+static int dispatch_prefill_f32_m(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
+    if (D == 128)
+        return causal ? launch_prefill_f32<128, true, MASKED>(p, stream) : launch_prefill_f32<128, false, MASKED>(p, stream);
+    if (D == 64)
+        return causal ? launch_prefill_f32<64, true, MASKED>(p, stream) : launch_prefill_f32<64, false, MASKED>(p, stream);
+    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %d not supported (64 or 128)", D);
+}
+
+// Entry from dtattn_prefill_fwd once the arguments are validated and `p` is filled.
+int prefill_f32(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
+    return p.mask != nullptr ? dispatch_prefill_f32_m<true>(p, D, causal, stream)
+                             : dispatch_prefill_f32_m<false>(p, D, causal, stream);
+}
+
+}  // namespace dtattn

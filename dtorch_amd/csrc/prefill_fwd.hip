@@ -28,42 +28,9 @@
 #include <stdio.h>
 
 #include "dtattn_common.hpp"
+#include "prefill_params.hpp"
 
 namespace dtattn {
-
-struct PrefillParams {
-    const void* q;
-    const void* k;
-    const void* v;
-    void* o;
-    float* lse;
-    int64_t qs_b, qs_h, qs_s;
-    int64_t ks_b, ks_h, ks_s;
-    int64_t vs_b, vs_h, vs_s;
-    int64_t os_b, os_h, os_s;
-    int64_t lses_b, lses_h;
-    int32_t B, Hq, Hkv, Sq, Sk, group;
-    int32_t n_qblocks;
-    int32_t delta;  // key j visible to query i iff j <= i + delta (causal only)
-    float c;        // softmax scale * log2(e)
-    int32_t xcd_map;  // 1: group the workgroups of each (batch, kv head) slice on one XCD
-    // additive fp32 attention mask (MASKED kernels): element (b, h, i, j) at
-    // mask + b*ms_b + h*ms_h + i*ms_l + j (key stride 1, strides multiples of 4, 16-byte aligned base);
-    // it enters the raw scores as m / scale, so -inf and the dtype-minimum fills both hide a key
-    const float* mask;
-    int64_t ms_b, ms_h, ms_l;
-    float inv_scale;
-};
-
-template <bool CAUSAL>
-__device__ __forceinline__ BlockCoord block_coord(const PrefillParams& p) {
-    return block_coord<CAUSAL>(p.B, p.Hq, p.Hkv, p.group, p.n_qblocks, p.xcd_map);
-}
-
-// Lazy rescaling: the running max only moves (and O, l are only rescaled) when some row's max grew
-// by more than 2^8; otherwise P is taken against the stale max (values up to 2^8, exact in the
-// normalisation, which uses the same max for O and l).
-constexpr float kRescaleThreshold = 8.0f;
 
 // XOR swizzle of the 16-byte chunk index of LDS row r (K and V tiles).  It is distinct over any 16
 // consecutive rows (the 16-byte K reads take one chunk of 16 rows per step) and differs above the
@@ -406,6 +373,7 @@ static int dispatch_prefill(const PrefillParams& p, int D, bool causal, hipStrea
 }
 
 int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_t stream);
+int prefill_f32(const PrefillParams& p, int D, bool causal, hipStream_t stream);
 
 static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
@@ -432,9 +400,10 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     if (a->q == nullptr || a->o == nullptr || (a->Sk > 0 && (a->k == nullptr || a->v == nullptr)))
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill: null tensor pointer");
     const int64_t* strides[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
-    const int esz_in = a->dtype == DTATTN_FP8_E4M3FN ? 1 : 2;
+    const int esz_in = a->dtype == DTATTN_FP8_E4M3FN ? 1 : (a->dtype == DTATTN_FP32 ? 4 : 2);
+    const int esz_out = a->o_dtype == DTATTN_FP32 ? 4 : 2;
     for (int i = 0; i < 4; ++i) {
-        const int esz = i == 3 ? 2 : esz_in;
+        const int esz = i == 3 ? esz_out : esz_in;
         for (int j = 0; j < 3; ++j)
             if ((strides[i][j] * esz) % 16 != 0)
                 return fail(DTATTN_ERR_UNSUPPORTED,
@@ -473,8 +442,9 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
             return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill fp8: descale pointers are required");
         return prefill_fp8(a, c, delta, stream);
     }
-    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16)
-        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: dtype %d not supported (bf16, fp16, fp8_e4m3fn)", a->dtype);
+    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16 && a->dtype != DTATTN_FP32)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: dtype %d not supported (bf16, fp16, fp32, fp8_e4m3fn)",
+                    a->dtype);
     if (a->o_dtype != a->dtype) return fail(DTATTN_ERR_UNSUPPORTED, "prefill: output dtype must equal input dtype");
 
     PrefillParams p;
@@ -504,6 +474,7 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     p.inv_scale = 1.0f / scale;
     const int D = (int)a->D;
     const bool causal = a->causal != 0;
+    if (a->dtype == DTATTN_FP32) return prefill_f32(p, D, causal, stream);
     if (a->dtype == DTATTN_BF16) return dispatch_prefill<bf16_t>(p, D, causal, stream);
     return dispatch_prefill<f16_t>(p, D, causal, stream);
 }

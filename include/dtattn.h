@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define DTATTN_ABI_VERSION 4
+#define DTATTN_ABI_VERSION 5
 
 typedef enum {
     DTATTN_OK = 0,
@@ -50,7 +50,9 @@ typedef enum {
  * visible to query i iff j + k_offset <= i + q_offset; (0, 0) is torch's top-left alignment, a ring
  * block uses the chunks' global offsets.  Rows that see no key get O = 0 and LSE = -inf.
  *
- * dtype: BF16 or FP16 (inputs and output), or FP8_E4M3FN inputs with descales and a BF16 output.
+ * dtype: BF16 or FP16 (inputs and output, fp32 softmax and accumulation); FP32 (inputs and output,
+ * every step in fp32: the fp32 matrix cores, no 16-bit rounding of P; ABI version 5); or FP8_E4M3FN
+ * inputs with descales and a BF16 output.
  * Head dims: D == Dv, D in {64, 128}.
  */
 typedef struct {
@@ -73,7 +75,7 @@ typedef struct {
     const float* q_descale; /* FP8 only: [B, Hq] fp32, real = code * descale */
     const float* k_descale; /* FP8 only: [B, Hkv] */
     const float* v_descale; /* FP8 only: [B, Hkv] */
-    /* Optional additive attention mask (BF16/FP16 only; NULL: none), the attn_mask of
+    /* Optional additive attention mask (BF16/FP16/FP32 inputs; NULL: none), the attn_mask of
      * scaled_dot_product_attention_op.cc:107-109 in float form: logits = scale * q.k + m, applied together
      * with the causal rule.  Element (b, h, i, j) is mask[b*mask_stride[0] + h*mask_stride[1] +
      * i*mask_stride[2] + j] (key stride 1; a stride of 0 broadcasts); strides are multiples of 4 and the

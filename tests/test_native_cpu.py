@@ -85,7 +85,9 @@ def _last_error():
     (dict(Hq=6, Hkv=4), 1, "multiple"),
     (dict(D=96, Dv=96), 2, "head dim"),
     (dict(Dv=64), 2, "Dv"),
-    (dict(dtype=3, o_dtype=3), 2, "dtype"),
+    (dict(dtype=5, o_dtype=5), 2, "dtype"),
+    (dict(dtype=3, o_dtype=0), 2, "output dtype"),                   # fp32 inputs need an fp32 output
+    (dict(dtype=3, o_dtype=3, q_stride=(ctypes.c_int64 * 3)(8 * 64 * 128, 64 * 128, 130)), 2, "16 bytes"),
     (dict(dtype=2, o_dtype=0), 1, "descale"),
     (dict(q=0), 1, "null"),
     (dict(Sq=-1), 1, "bad sizes"),
