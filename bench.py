@@ -6,7 +6,8 @@ S=2048, D=128, bf16), inputs resident in HBM.  ``value`` is algorithmic TFLOP/s 
 4*B*Hq*D*S(S+1)/2) over the timed steps.  Also reported, each on its own synthetic inputs: split-KV
 decode HBM GB/s (B=64, Hq=32, Hkv=8, D=128, lengths U[512, 8192]) with a contiguous and a paged cache,
 one decode step (KV-cache append of one token + decode), the ring step (4 blocks + LSE merge), MMDiT
-joint attention in bf16 and fp8, and the fp32-spec causal MHA case.  The CPU baseline is
+joint attention in bf16 and fp8, the small causal MHA case in fp32 and bf16, and fp32 prefill on the
+headline shape.  The CPU baseline is
 libtorch's CPU SDPA in bf16 (the call SdpaOp::Compute makes on a CPU mesh) on the same prefill, timed
 on this host over about ten seconds of repetitions, and compared with the GPU output.
 
@@ -33,6 +34,7 @@ if ROOT not in sys.path:
 PEAK_BF16 = 2.5e15   # MI355X dense bf16 MFMA, FLOP/s (published)
 PEAK_FP8 = 5.0e15    # MI355X dense fp8 MFMA
 PEAK_HBM = 8.0e12    # MI355X HBM3E, B/s
+PEAK_FP32 = 157.3e12  # MI355X dense fp32 MFMA
 
 # HBM bytes per launch of the headline kernel, from the two calibrated rocprofv3 --pmc runs
 # (FETCH_SIZE, WRITE_SIZE) summarised in this file.
@@ -222,11 +224,25 @@ def secondary_workloads(torch, F, dev, timer):
         f"(quantize {med_q * 1e6:.0f} us, attention ~{f5 / kern8 / 1e12:.0f} TFLOP/s)")
     del q5, k5, v5
 
-    # fp32-spec causal MHA (runs in bf16 on the GPU)
-    q1, k1, v1 = (torch.randn(1, 8, 512, 64, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    # the CPU-runnable causal MHA case (B=1, H=8, S=512, D=64) in its own dtype, fp32, and in bf16
+    q1, k1, v1 = (torch.randn(1, 8, 512, 64, device=dev, generator=g) for _ in range(3))
     f1 = causal_flops(1, 8, 512, 64)
+    med32, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q1, k1, v1, is_causal=True), reps=20)
+    q1, k1, v1 = (x.to(torch.bfloat16) for x in (q1, k1, v1))
     med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q1, k1, v1, is_causal=True), reps=20)
-    extras["c1_causal_mha_d64"] = {"TFLOP/s": round(f1 / med / 1e12, 2), "us": round(med * 1e6, 1)}
+    extras["c1_causal_mha_d64"] = {"TFLOP/s_fp32": round(f1 / med32 / 1e12, 2), "us_fp32": round(med32 * 1e6, 1),
+                                   "TFLOP/s_bf16": round(f1 / med / 1e12, 2), "us_bf16": round(med * 1e6, 1)}
+    del q1, k1, v1
+
+    # fp32 prefill on the headline shape (fp32 inputs are computed in fp32 on the fp32 matrix cores)
+    qf, kf, vf = (torch.randn(4, h, 2048, 128, device=dev, generator=g) for h in (32, 8, 8))
+    f2 = causal_flops(4, 32, 2048, 128)
+    med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(qf, kf, vf, is_causal=True, enable_gqa=True),
+                       reps=10)
+    extras["prefill_c2_shape_fp32"] = {"TFLOP/s": round(f2 / med / 1e12, 1), "frac_fp32": round(f2 / med / PEAK_FP32, 4),
+                                       "us": round(med * 1e6, 1)}
+    log(f"fp32 prefill 4x32x2048 causal GQA: {f2 / med / 1e12:.1f} TFLOP/s ({f2 / med / PEAK_FP32 * 100:.1f}% of fp32 peak)")
+    del qf, kf, vf
     del flush_buf
     return extras
 
@@ -286,18 +302,20 @@ def main():
     for _ in range(args.warmup):
         out = step()
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # One event pair on the launch stream brackets the K launches: their GPU time over K is the average
+    # launch duration (it includes the dispatch gaps, so it bounds the kernel time from above).  An event
+    # pair per step would add ~7 us of event packets to every step (measured: 147 -> 154 us per step).
+    e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for s_, e_ in evs:
-        s_.record()
+    e_start.record()
+    for _ in range(args.steps):
         out = step()
-        e_.record()
+    e_end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kern = [s_.elapsed_time(e_) * 1e-3 for s_, e_ in evs]
     ms_per_step = wall / args.steps * 1e3
     value = flops / (wall / args.steps) / 1e12
-    k_avg = float(np.mean(kern))
+    k_avg = e_start.elapsed_time(e_end) * 1e-3 / args.steps
     achieved = flops / k_avg / 1e12
     log(f"prefill causal GQA B=4 Hq=32 Hkv=8 S=2048 D=128 bf16: {ms_per_step:.3f} ms/step wall, kernel avg "
         f"{k_avg * 1e6:.1f} us -> {achieved:.1f} TFLOP/s ({100 * achieved * 1e12 / PEAK_BF16:.1f}% of bf16 peak)")
