@@ -65,9 +65,11 @@ size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t 
 // otherwise through a buffer resource over the chunk's rows.
 template <typename T, int D, int G, int TPW, bool PAGED>
 __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
-    constexpr int LPT = D / 8;            // lanes per token row
+    constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk: 8 (bf16, fp16) or 4 (fp32)
+    constexpr int LPT = D / EPC;          // lanes per token row
     constexpr int TPI = 64 / LPT;         // tokens per wave-wide load
-    constexpr int SB = TPW < 64 ? TPW : 64;
+    constexpr int SBMAX = 16 * TPI < 64 ? 16 * TPI : 64;  // at most 64 tokens and 16 K + 16 V loads per lane
+    constexpr int SB = TPW < SBMAX ? TPW : SBMAX;
     constexpr int NSB = TPW / SB;         // sub-blocks per wave
     constexpr int NI = SB / TPI;          // K (and V) loads per lane per sub-block
     constexpr int C = 4 * TPW;
@@ -104,7 +106,7 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     u32x4 qv[G];
 #pragma unroll
     for (int g = 0; g < G; ++g)
-        qv[g] = ld16(reinterpret_cast<const T*>(p.q) + b * p.qs_b + (hq0 + g) * p.qs_h + c8 * 8);
+        qv[g] = ld16(reinterpret_cast<const T*>(p.q) + b * p.qs_b + (hq0 + g) * p.qs_h + c8 * EPC);
 
     const int kpitch = (int)(p.ks_s * (int64_t)sizeof(T));
     const int vpitch = (int)(p.vs_s * (int64_t)sizeof(T));
@@ -116,13 +118,13 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     const auto vrs = make_rsrc(vp, (uint32_t)((n_tok - 1) * vpitch + D * (int)sizeof(T)));
     const int32_t* bt = PAGED ? p.block_table + b * p.bt_s : nullptr;
 
-    float m[G], l[G], acc[G][8];
+    float m[G], l[G], acc[G][EPC];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m[g] = kNegInf;
         l[g] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+        for (int e = 0; e < EPC; ++e) acc[g][e] = 0.f;
     }
 
 #pragma unroll
@@ -142,8 +144,8 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
             const int rmask = (1 << p.page_shift) - 1;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {  // the cache is read once per call
-                kr[i] = ld16_nt(kp + pg[i] * p.ks_b + (tr[i] & rmask) * p.ks_s + c8 * 8);
-                vr[i] = ld16_nt(vp + pg[i] * p.vs_b + (tr[i] & rmask) * p.vs_s + c8 * 8);
+                kr[i] = ld16_nt(kp + pg[i] * p.ks_b + (tr[i] & rmask) * p.ks_s + c8 * EPC);
+                vr[i] = ld16_nt(vp + pg[i] * p.vs_b + (tr[i] & rmask) * p.vs_s + c8 * EPC);
             }
         } else {
 #pragma unroll
@@ -164,10 +166,18 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 float a = 0.f;
-                a = Elem<T>::dot2(kr[i].x, qv[g].x, a);
-                a = Elem<T>::dot2(kr[i].y, qv[g].y, a);
-                a = Elem<T>::dot2(kr[i].z, qv[g].z, a);
-                a = Elem<T>::dot2(kr[i].w, qv[g].w, a);
+                if constexpr (EPC == 8) {
+                    a = Elem<T>::dot2(kr[i].x, qv[g].x, a);
+                    a = Elem<T>::dot2(kr[i].y, qv[g].y, a);
+                    a = Elem<T>::dot2(kr[i].z, qv[g].z, a);
+                    a = Elem<T>::dot2(kr[i].w, qv[g].w, a);
+                } else {
+                    const f32x4 kf = __builtin_bit_cast(f32x4, kr[i]), qf = __builtin_bit_cast(f32x4, qv[g]);
+                    a = __builtin_fmaf(kf.x, qf.x, a);
+                    a = __builtin_fmaf(kf.y, qf.y, a);
+                    a = __builtin_fmaf(kf.z, qf.z, a);
+                    a = __builtin_fmaf(kf.w, qf.w, a);
+                }
                 a = group_sum<LPT>(a);
                 sc[i][g] = ok ? a * p.c : kNegInf;
             }
@@ -184,7 +194,7 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
             m[g] = mnew;
             float ls = l[g] * alpha;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
+            for (int e = 0; e < EPC; ++e) acc[g][e] *= alpha;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const float pw = fast_exp2(sc[i][g] - mbase);
@@ -193,21 +203,35 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
             }
             l[g] = ls;
         }
-        // P V over token pairs (loads i, i+1 hold tokens t, t+TPI of the same row chunk): pack
-        // (v_t[e], v_t'[e]) and (p_t, p_t') as element pairs and accumulate with v_dot2.
+        if constexpr (EPC == 8) {
+            // P V over token pairs (loads i, i+1 hold tokens t, t+TPI of the same row chunk): pack
+            // (v_t[e], v_t'[e]) and (p_t, p_t') as element pairs and accumulate with v_dot2.
 #pragma unroll
-        for (int i = 0; i < NI; i += 2) {
-            uint32_t vp2[8];
+            for (int i = 0; i < NI; i += 2) {
+                uint32_t vp2[8];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                vp2[2 * w] = pack_lo_hi(vr[i][w], vr[i + 1][w], 0);
-                vp2[2 * w + 1] = pack_lo_hi(vr[i][w], vr[i + 1][w], 1);
+                for (int w = 0; w < 4; ++w) {
+                    vp2[2 * w] = pack_lo_hi(vr[i][w], vr[i + 1][w], 0);
+                    vp2[2 * w + 1] = pack_lo_hi(vr[i][w], vr[i + 1][w], 1);
+                }
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const uint32_t pp = pack2<T>(sc[i][g], sc[i + 1][g]);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[g][e] = Elem<T>::dot2(vp2[e], pp, acc[g][e]);
+                }
             }
+        } else {  // fp32: P and V stay fp32
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const uint32_t pp = pack2<T>(sc[i][g], sc[i + 1][g]);
+            for (int i = 0; i < NI; ++i) {
+                const f32x4 vf = __builtin_bit_cast(f32x4, vr[i]);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] = Elem<T>::dot2(vp2[e], pp, acc[g][e]);
+                for (int g = 0; g < G; ++g) {
+                    acc[g][0] = __builtin_fmaf(sc[i][g], vf.x, acc[g][0]);
+                    acc[g][1] = __builtin_fmaf(sc[i][g], vf.y, acc[g][1]);
+                    acc[g][2] = __builtin_fmaf(sc[i][g], vf.z, acc[g][2]);
+                    acc[g][3] = __builtin_fmaf(sc[i][g], vf.w, acc[g][3]);
+                }
             }
         }
     }
@@ -216,13 +240,13 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     for (int g = 0; g < G; ++g) {
         l[g] = sum_across_groups<LPT>(l[g]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = sum_across_groups<LPT>(acc[g][e]);
+        for (int e = 0; e < EPC; ++e) acc[g][e] = sum_across_groups<LPT>(acc[g][e]);
     }
     if (tsub == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) red_o[wave][g][c8 * 8 + e] = acc[g][e];
+            for (int e = 0; e < EPC; ++e) red_o[wave][g][c8 * EPC + e] = acc[g][e];
     }
     if (lane == 0) {
 #pragma unroll
@@ -366,17 +390,17 @@ extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: bad sizes");
     if (a->Hq % a->Hkv != 0) return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: Hq is not a multiple of Hkv");
     if (a->B == 0) return DTATTN_OK;
-    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16)
-        return fail(DTATTN_ERR_UNSUPPORTED, "decode: dtype %d not supported (bf16, fp16)", a->dtype);
+    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16 && a->dtype != DTATTN_FP32)
+        return fail(DTATTN_ERR_UNSUPPORTED, "decode: dtype %d not supported (bf16, fp16, fp32)", a->dtype);
+    const int64_t esz = a->dtype == DTATTN_FP32 ? 4 : 2;
     const int32_t chunk = a->chunk > 0 ? a->chunk : auto_chunk(a->Hq, a->Hkv);
     if (chunk != 128 && chunk != 256 && chunk != 512)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: chunk %d must be 128, 256 or 512", chunk);
     // chunk rows are addressed with 32-bit byte offsets
-    if (a->k_stride[2] * 2 * chunk >= ((int64_t)1 << 31) || a->v_stride[2] * 2 * chunk >= ((int64_t)1 << 31))
+    if (a->k_stride[2] * esz * chunk >= ((int64_t)1 << 31) || a->v_stride[2] * esz * chunk >= ((int64_t)1 << 31))
         return fail(DTATTN_ERR_UNSUPPORTED, "decode: cache row pitch too large");
     if (a->q == nullptr || a->k_cache == nullptr || a->v_cache == nullptr || a->lengths == nullptr || a->o == nullptr)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: null pointer");
-    const int64_t esz = 2;
     const int64_t s_all[] = {a->q_stride[0], a->q_stride[1], a->k_stride[0], a->k_stride[1], a->k_stride[2],
                              a->v_stride[0], a->v_stride[1], a->v_stride[2]};
     for (int64_t s : s_all)
@@ -419,6 +443,7 @@ extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_)
     p.page_shift = 0;
     p.num_pages = 0;
     if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, false>(p, (int)a->D, stream);
+    if (a->dtype == DTATTN_FP32) return dispatch_decode<float, false>(p, (int)a->D, stream);
     return dispatch_decode<f16_t, false>(p, (int)a->D, stream);
 }
 
@@ -442,15 +467,15 @@ extern "C" int dtattn_decode_paged(const dtattn_decode_paged_args* a, void* stre
     if (S_max > (1 << 29) || a->num_pages > 0x7fffffff)
         return fail(DTATTN_ERR_UNSUPPORTED, "decode_paged: cache too large");
     if (a->B == 0) return DTATTN_OK;
-    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16)
-        return fail(DTATTN_ERR_UNSUPPORTED, "decode_paged: dtype %d not supported (bf16, fp16)", a->dtype);
+    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16 && a->dtype != DTATTN_FP32)
+        return fail(DTATTN_ERR_UNSUPPORTED, "decode_paged: dtype %d not supported (bf16, fp16, fp32)", a->dtype);
     const int32_t chunk = a->chunk > 0 ? a->chunk : auto_chunk(a->Hq, a->Hkv);
     if (chunk != 128 && chunk != 256 && chunk != 512)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: chunk %d must be 128, 256 or 512", chunk);
     if (a->q == nullptr || a->k_pages == nullptr || a->v_pages == nullptr || a->block_table == nullptr ||
         a->lengths == nullptr || a->o == nullptr)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: null pointer");
-    const int64_t esz = 2;
+    const int64_t esz = a->dtype == DTATTN_FP32 ? 4 : 2;
     const int64_t s_all[] = {a->q_stride[0], a->q_stride[1], a->k_stride[0], a->k_stride[1], a->k_stride[2],
                              a->v_stride[0], a->v_stride[1], a->v_stride[2]};
     for (int64_t s : s_all)
@@ -494,5 +519,6 @@ extern "C" int dtattn_decode_paged(const dtattn_decode_paged_args* a, void* stre
     p.page_shift = __builtin_ctzll((unsigned long long)a->page_size);
     p.num_pages = (int32_t)a->num_pages;
     if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, true>(p, (int)a->D, stream);
+    if (a->dtype == DTATTN_FP32) return dispatch_decode<float, true>(p, (int)a->D, stream);
     return dispatch_decode<f16_t, true>(p, (int)a->D, stream);
 }

@@ -48,6 +48,13 @@ struct Elem<bf16_t> {
     }
 };
 
+// fp32 elements (decode and append of fp32 caches): conversions only.
+template <>
+struct Elem<float> {
+    static __device__ __forceinline__ float to_f32(float x) { return x; }
+    static __device__ __forceinline__ float from_f32(float x) { return x; }
+};
+
 template <>
 struct Elem<f16_t> {
     typedef f16x8 vec8;
@@ -190,17 +197,6 @@ constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141; // lane i <- lane 7-i within each half row
 constexpr int kDppRowMirror = 0x140;     // lane i <- lane 15-i within the row
 
-// Sum over aligned groups of N lanes (N = 8 or 16); every lane of the group receives the total.
-template <int N>
-__device__ __forceinline__ float group_sum(float x) {
-    static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
-    x += dpp_f<kDppQuadXor1>(x);
-    x += dpp_f<kDppQuadXor2>(x);
-    x += dpp_f<kDppRowHalfMirror>(x);
-    if (N == 16) x += dpp_f<kDppRowMirror>(x);
-    return x;
-}
-
 // Cross-row exchanges on gfx950 (VALU, no LDS round trip).  v_permlane32_swap with both operands
 // equal to x returns {x[l], x[l^32]} in some order in every lane, and v_permlane16_swap returns
 // {x[l], x[l^16]}; combining the pair with a commutative op is the xor-32 / xor-16 butterfly step.
@@ -237,14 +233,28 @@ __device__ __forceinline__ float sum_xor16(float x) {
     return a + b;
 }
 
-// Reductions over the lanes that share lane % N (N = 8 or 16), i.e. across the 64/N lane groups.
+// Sum over aligned groups of N lanes (N = 8, 16 or 32); every lane of the group receives the total.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+    static_assert(N == 8 || N == 16 || N == 32, "group of 8, 16 or 32 lanes");
+    x += dpp_f<kDppQuadXor1>(x);
+    x += dpp_f<kDppQuadXor2>(x);
+    x += dpp_f<kDppRowHalfMirror>(x);
+    if (N >= 16) x += dpp_f<kDppRowMirror>(x);
+    if (N == 32) x = sum_xor16(x);
+    return x;
+}
+
+// Reductions over the lanes that share lane % N (N = 8, 16 or 32), i.e. across the 64/N lane groups.
 template <int N>
 __device__ __forceinline__ float sum_across_groups(float x) {
+    if (N == 32) return sum_xor32(x);
     if (N == 8) x += dpp_f<0x128>(x);  // row_ror:8 == lane ^ 8 within a row of 16
     return sum_xor32(sum_xor16(x));
 }
 template <int N>
 __device__ __forceinline__ float max_across_groups(float x) {
+    if (N == 32) return max_xor32(x);
     if (N == 8) x = fmaxf(x, dpp_f<0x128>(x));
     return max_xor32(max_xor16(x));
 }

@@ -339,7 +339,7 @@ void SdpaDecodeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& 
         Throw("lengths must be an int32 tensor of shape [B]");
     const c10::ScalarType st = q.scalar_type();
     if (kc.scalar_type() != st || vc.scalar_type() != st) Throw("query and cache dtypes differ");
-    if (st != at::kBFloat16 && st != at::kHalf) Throw("decode supports bf16 and fp16");
+    if (st != at::kBFloat16 && st != at::kHalf && st != at::kFloat) Throw("decode supports bf16, fp16 and fp32");
     if (mScale.has_value() && !(mScale.value() > 0.0)) Throw("scale must be positive");
 
     at::Tensor o = at::empty(q.sizes(), q.options());
@@ -398,7 +398,8 @@ NewTokens CheckNewTokens(const at::Tensor& kn, const at::Tensor& vn, const at::T
         Throw("k_new must be [B, Hkv, n_new, D] matching the cache");
     if (kn.scalar_type() != kc.scalar_type() || vn.scalar_type() != kc.scalar_type())
         Throw("new tokens and cache dtypes differ");
-    if (kc.scalar_type() != at::kBFloat16 && kc.scalar_type() != at::kHalf) Throw("the KV cache must be bf16 or fp16");
+    if (kc.scalar_type() != at::kBFloat16 && kc.scalar_type() != at::kHalf && kc.scalar_type() != at::kFloat)
+        Throw("the KV cache must be bf16, fp16 or fp32");
     NewTokens r;
     r.k = MakeView4(kn, "k_new");
     r.v = MakeView4(vn, "v_new");
@@ -493,7 +494,7 @@ void SdpaDecodePagedOp::Compute(const TorchTensorOptArray& inputs, TorchTensorAr
         Throw("lengths must be an int32 tensor of shape [B]");
     const c10::ScalarType st = q.scalar_type();
     if (kp.scalar_type() != st || vp.scalar_type() != st) Throw("query and page dtypes differ");
-    if (st != at::kBFloat16 && st != at::kHalf) Throw("decode supports bf16 and fp16");
+    if (st != at::kBFloat16 && st != at::kHalf && st != at::kFloat) Throw("decode supports bf16, fp16 and fp32");
     if (mScale.has_value() && !(mScale.value() > 0.0)) Throw("scale must be positive");
     if (kp.stride(3) != 1 || vp.stride(3) != 1) Throw("page pools need a unit stride along D");
 

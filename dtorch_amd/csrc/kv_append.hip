@@ -86,16 +86,19 @@ static int common_append(AppendParams& p, const void* k_new, const void* v_new, 
                          const int64_t ks[3], const int64_t vs[3], int32_t dtype, const char* who) {
     if (B < 0 || Hkv <= 0 || n_new < 0 || D <= 0)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "%s: bad sizes", who);
-    if (dtype != DTATTN_BF16 && dtype != DTATTN_FP16)
-        return fail(DTATTN_ERR_UNSUPPORTED, "%s: dtype %d not supported (bf16, fp16)", who, dtype);
-    if (D % 8 != 0) return fail(DTATTN_ERR_UNSUPPORTED, "%s: D=%lld must be a multiple of 8", who, (long long)D);
+    if (dtype != DTATTN_BF16 && dtype != DTATTN_FP16 && dtype != DTATTN_FP32)
+        return fail(DTATTN_ERR_UNSUPPORTED, "%s: dtype %d not supported (bf16, fp16, fp32)", who, dtype);
+    const int esz = dtype == DTATTN_FP32 ? 4 : 2;
+    if ((D * esz) % 16 != 0)
+        return fail(DTATTN_ERR_UNSUPPORTED, "%s: a token row of D=%lld elements is not a multiple of 16 bytes", who,
+                    (long long)D);
     if (n_new > 0x3fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "%s: too many new tokens", who);
     if (lengths == nullptr || (B > 0 && n_new > 0 && (k_new == nullptr || v_new == nullptr)))
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "%s: null pointer", who);
     const int64_t* all[4] = {kn, vn, ks, vs};
     for (int i = 0; i < 4; ++i)
         for (int s = 0; s < 3; ++s)
-            if ((all[i][s] * 2) % 16 != 0)
+            if ((all[i][s] * esz) % 16 != 0)
                 return fail(DTATTN_ERR_UNSUPPORTED, "%s: strides must be multiples of 16 bytes", who);
     if ((reinterpret_cast<uintptr_t>(k_new) | reinterpret_cast<uintptr_t>(v_new)) & 15u)
         return fail(DTATTN_ERR_UNSUPPORTED, "%s: new tokens must be 16-byte aligned", who);
@@ -109,8 +112,8 @@ static int common_append(AppendParams& p, const void* k_new, const void* v_new, 
     p.rows = B * Hkv * n_new;
     p.Hkv = (int32_t)Hkv;
     p.n_new = (int32_t)n_new;
-    p.cpr = (int32_t)(D / 8);
-    p.esz = 2;
+    p.cpr = (int32_t)(D * esz / 16);
+    p.esz = esz;
     return DTATTN_OK;
 }
 

@@ -108,7 +108,7 @@ typedef struct {
     int64_t v_stride[3];
     int64_t o_stride[2];   /* B, H */
     int64_t lse_stride[1]; /* B (H stride is 1) */
-    int32_t dtype;         /* BF16 or FP16 */
+    int32_t dtype;         /* BF16, FP16 or FP32 (FP32 from ABI version 5) */
     float scale;           /* <= 0 means 1/sqrt(D) */
     int32_t chunk;         /* tokens per split: 128, 256 or 512; 0 picks 256 (128 when Hq / Hkv is a
                               multiple of 8 and Hkv is not); workspace sizes for chunk 0 cover it */
@@ -143,7 +143,7 @@ typedef struct {
     int64_t o_stride[2];       /* B, H */
     int64_t lse_stride[1];     /* B (H stride is 1) */
     int64_t block_table_stride;/* elements between rows of block_table */
-    int32_t dtype;             /* BF16 or FP16 */
+    int32_t dtype;             /* BF16, FP16 or FP32 (FP32 from ABI version 5) */
     float scale;               /* <= 0 means 1/sqrt(D) */
     int32_t chunk;             /* tokens per split: 128, 256 or 512; 0 picks as dtattn_decode_args does */
     void* workspace;           /* >= dtattn_decode_paged_workspace_size(...) bytes, 256-byte aligned */
@@ -162,7 +162,8 @@ int dtattn_decode_paged(const dtattn_decode_paged_args* args, void* stream);
  * listed as the next step for decode.  Token j (0 <= j < n_new) of sequence b goes to cache position
  * t = max(lengths[b], 0) + j; positions at or past the capacity are not written.  Afterwards, in stream
  * order, lengths[b] = min(max(lengths[b], 0) + n_new, capacity): callers that must not drop tokens check
- * the capacity on the host.  dtype BF16 or FP16 for new tokens and cache alike; D a multiple of 8.
+ * the capacity on the host.  dtype BF16, FP16 or FP32 (ABI version 5) for new tokens and cache alike; a
+ * token row of D elements a multiple of 16 bytes.
  */
 typedef struct {
     const void* k_new;     /* [B, Hkv, n_new, D] (any strides, D stride 1) */

@@ -194,7 +194,10 @@ def test_kv_append_validation():
     a.dtype = 2  # fp8 is not a cache dtype
     assert lib.dtattn_kv_append(ctypes.byref(a), None) == 2 and "dtype" in _last_error()
     a.dtype, a.D = 0, 12
-    assert lib.dtattn_kv_append(ctypes.byref(a), None) == 2 and "multiple of 8" in _last_error()
+    assert lib.dtattn_kv_append(ctypes.byref(a), None) == 2 and "multiple of 16 bytes" in _last_error()
+    a.dtype, a.D = 3, 6  # fp32 rows of 6 elements: 24 bytes
+    assert lib.dtattn_kv_append(ctypes.byref(a), None) == 2 and "multiple of 16 bytes" in _last_error()
+    a.dtype = 0
     a.D = 128
     assert lib.dtattn_kv_append(ctypes.byref(a), None) == 1 and "null" in _last_error()
     a.k_new = a.v_new = a.lengths = 4096  # never dereferenced: the stride check fails first
