@@ -282,8 +282,8 @@ struct BlockCoord {
 };
 
 template <bool CAUSAL>
-__device__ __forceinline__ BlockCoord block_coord(int B, int Hq, int Hkv, int group, int n_qblocks, int xcd_map) {
-    const int bid = blockIdx.x;
+__device__ __forceinline__ BlockCoord block_coord_at(int bid, int B, int Hq, int Hkv, int group, int n_qblocks,
+                                                     int xcd_map) {
     BlockCoord r;
     if (xcd_map) {
         const int x = bid & 7, j = bid >> 3;
@@ -303,6 +303,11 @@ __device__ __forceinline__ BlockCoord block_coord(int B, int Hq, int Hkv, int gr
         r.hk = r.hq / group;
     }
     return r;
+}
+
+template <bool CAUSAL>
+__device__ __forceinline__ BlockCoord block_coord(int B, int Hq, int Hkv, int group, int n_qblocks, int xcd_map) {
+    return block_coord_at<CAUSAL>(blockIdx.x, B, Hq, Hkv, group, n_qblocks, xcd_map);
 }
 
 // ---- host-side status plumbing ----------------------------------------------------------------
