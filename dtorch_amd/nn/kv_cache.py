@@ -37,15 +37,13 @@ class KVCache:
     def capacity(self) -> int:
         return self.k.shape[2]
 
-    def _reserve(self, n: int) -> None:
-        if int(self._host_len.max(initial=0)) + n > self.capacity:
-            raise ValueError(f"KV cache full: {int(self._host_len.max())} + {n} tokens > capacity {self.capacity}")
-        self._host_len += n
-
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
         """Append [B, Hkv, n, D] keys and values after each sequence's current length."""
-        self._reserve(k_new.shape[2])
+        n = k_new.shape[2]
+        if int(self._host_len.max(initial=0)) + n > self.capacity:
+            raise ValueError(f"KV cache full: {int(self._host_len.max())} + {n} tokens > capacity {self.capacity}")
         F.kv_cache_append(self.k, self.v, self.lengths, k_new, v_new)
+        self._host_len += n  # only once the append was accepted
 
     def prefill(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         """Causal attention over a prompt of equal length per sequence (the cache must be empty for the
@@ -97,8 +95,8 @@ class PagedKVCache:
                 changed = True
         if changed:
             self.block_table.copy_(torch.from_numpy(self._table), non_blocking=False)
-        self._host_len += n
         F.kv_cache_append_paged(self.k, self.v, self.block_table, self.lengths, k_new, v_new)
+        self._host_len += n  # only once the append was accepted
 
     def prefill(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         if int(self._host_len.max(initial=0)) != 0:
