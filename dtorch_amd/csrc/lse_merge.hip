@@ -5,6 +5,8 @@
 //   m = max_b LSE_b,  LSE = m + log sum_b exp(LSE_b - m),  O = sum_b exp(LSE_b - LSE) O_b.
 // HBM-bound: one thread per 16-byte output chunk (8 elements); each thread reads the n LSE values of
 // its row (shared by the D/8 threads of the row through L1) and n input chunks, and writes one chunk.
+// A workgroup covers 256 consecutive chunks of one (batch, head) slab, so the only divisions are
+// per workgroup and scalar; a thread's row and chunk come from shifts.
 #include "dtattn_common.hpp"
 
 namespace dtattn {
@@ -18,8 +20,9 @@ struct MergeParams {
     int64_t bl_b, bl_h;
     int64_t o_b, o_h, o_s;
     int64_t l_b, l_h;
-    int64_t rows;  // B * H * S
+    int64_t slabs;  // B * H
     int32_t H, S, n;
+    int32_t wg_per_slab;  // ceil(S * D / 8 / 256)
 };
 
 // Block outputs are read exactly once: non-temporal loads (load_chunk<TI, true>).
@@ -42,13 +45,11 @@ __device__ __forceinline__ void store8<float>(float* p, const float* in) {
 
 template <typename TI, typename TO, int D, int NB>
 __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeParams p) {
-    constexpr int CPR = D / 8;  // chunks per row
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t row = gid / CPR;
-    if (row >= p.rows) return;
-    const int c = (int)(gid % CPR);
-    const int s = (int)(row % p.S);
-    const int64_t bh = row / p.S;
+    constexpr int CPR = D / 8;  // chunks per row (a power of two)
+    const int64_t bh = blockIdx.x / p.wg_per_slab;  // wave-uniform
+    const int idx = (int)(blockIdx.x - bh * p.wg_per_slab) * 256 + (int)threadIdx.x;
+    const int s = idx / CPR, c = idx % CPR;
+    if (s >= p.S) return;
     const int h = (int)(bh % p.H);
     const int64_t b = bh / p.H;
     const int n = NB > 0 ? NB : p.n;
@@ -117,19 +118,20 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeParams p) {
 
 template <typename TI, typename TO, int D>
 static int launch_merge(const MergeParams& p, hipStream_t stream) {
-    const int64_t threads = p.rows * (D / 8);
-    const int64_t blocks = (threads + 255) / 256;
+    MergeParams q = p;
+    q.wg_per_slab = (int32_t)(((int64_t)p.S * (D / 8) + 255) / 256);
+    const int64_t blocks = p.slabs * q.wg_per_slab;
     if (blocks == 0) return DTATTN_OK;
     if (blocks > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "merge: grid too large");
     switch (p.n) {
         case 2:
-            hipLaunchKernelGGL((lse_merge_kernel<TI, TO, D, 2>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+            hipLaunchKernelGGL((lse_merge_kernel<TI, TO, D, 2>), dim3((unsigned)blocks), dim3(256), 0, stream, q);
             break;
         case 4:
-            hipLaunchKernelGGL((lse_merge_kernel<TI, TO, D, 4>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+            hipLaunchKernelGGL((lse_merge_kernel<TI, TO, D, 4>), dim3((unsigned)blocks), dim3(256), 0, stream, q);
             break;
         default:
-            hipLaunchKernelGGL((lse_merge_kernel<TI, TO, D, 0>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+            hipLaunchKernelGGL((lse_merge_kernel<TI, TO, D, 0>), dim3((unsigned)blocks), dim3(256), 0, stream, q);
             break;
     }
     return check_launch("lse_merge_kernel");
@@ -162,7 +164,7 @@ extern "C" int dtattn_lse_merge(const dtattn_merge_args* a, void* stream_) {
                     DTATTN_MAX_MERGE_BLOCKS);
     if (a->B < 0 || a->H < 0 || a->S < 0 || a->D <= 0) return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: bad sizes");
     if (a->B == 0 || a->H == 0 || a->S == 0) return DTATTN_OK;
-    if (a->S > 0x7fffffff || a->H > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "merge: sizes too large");
+    if (a->S > (1 << 26) || a->H > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "merge: sizes too large");
     if (a->o == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: null output");
     const int in_esz = a->block_dtype == DTATTN_FP32 ? 4 : 2;
     const int out_esz = a->o_dtype == DTATTN_FP32 ? 4 : 2;
@@ -186,7 +188,8 @@ extern "C" int dtattn_lse_merge(const dtattn_merge_args* a, void* stream_) {
     p.o_b = a->o_stride[0], p.o_h = a->o_stride[1], p.o_s = a->o_stride[2];
     p.l_b = a->lse ? a->lse_stride[0] : 0;
     p.l_h = a->lse ? a->lse_stride[1] : 0;
-    p.rows = a->B * a->H * a->S;
+    p.slabs = a->B * a->H;
+    p.wg_per_slab = 0;
     p.H = (int32_t)a->H;
     p.S = (int32_t)a->S;
     p.n = a->n_blocks;
