@@ -5,7 +5,7 @@ Step = one causal GQA prefill forward with LSE on the Llama-3-8B attention shape
 S=2048, D=128, bf16), inputs resident in HBM.  ``value`` is algorithmic TFLOP/s (visible pairs only:
 4*B*Hq*D*S(S+1)/2) over the timed steps.  Also reported, each on its own synthetic inputs: split-KV
 decode HBM GB/s (B=64, Hq=32, Hkv=8, D=128, lengths U[512, 8192]) with a contiguous and a paged cache,
-one decode step (KV-cache append of one token + decode), the ring step (4 blocks + LSE merge), MMDiT
+one decode step (KV-cache append of one token + decode), eager and as a HIP graph replay, the ring step (4 blocks + LSE merge), MMDiT
 joint attention in bf16 and fp8, the small causal MHA case in fp32 and bf16, and fp32 prefill on the
 headline shape.  The CPU baseline is
 libtorch's CPU SDPA in bf16 (the call SdpaOp::Compute makes on a CPU mesh) on the same prefill, timed
@@ -157,6 +157,36 @@ def secondary_workloads(torch, F, dev, timer):
     extras["decode_step_c3"] = {"us": round(med_s * 1e6, 1), "GB/s": round(dbytes / med_s / 1e9, 1),
                                 "note": "kv_cache_append of 1 token per sequence + decode_attention"}
     log(f"decode step (append 1 token + decode): {med_s * 1e6:.1f} us")
+
+    # a launch-bound decode step (one sequence, 4096 cached tokens, 32/8 heads): eager calls against one
+    # replay of the same step captured in a HIP graph (the kernels allocate nothing and read the lengths
+    # from device memory, so the graph replays them as they are)
+    kq = torch.randn(1, Hkvd, 4096, Dd, device=dev, generator=g).to(torch.bfloat16)
+    vq = torch.randn(1, Hkvd, 4096, Dd, device=dev, generator=g).to(torch.bfloat16)
+    q_1 = torch.randn(1, Hqd, 1, Dd, device=dev, generator=g).to(torch.bfloat16)
+    kn_1 = torch.randn(1, Hkvd, 1, Dd, device=dev, generator=g).to(torch.bfloat16)
+    vn_1 = torch.randn(1, Hkvd, 1, Dd, device=dev, generator=g).to(torch.bfloat16)
+    len_1 = torch.full((1,), 4095, dtype=torch.int32, device=dev)
+
+    def step_1():
+        F.kv_cache_append(kq, vq, len_1, kn_1, vn_1)
+        return F.decode_attention(q_1, kq, vq, len_1)
+
+    def reset_1():
+        len_1.fill_(4095)
+
+    med_e, _ = timer.run(step_1, reps=50, flush=reset_1)
+    reset_1()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step_1()
+    med_g, _ = timer.run(graph.replay, reps=50, flush=reset_1)
+    extras["decode_step_b1_4k"] = {"us_eager": round(med_e * 1e6, 1), "us_graph": round(med_g * 1e6, 1),
+                                   "note": "one sequence, 4096 cached tokens, 32/8 heads: append + decode, "
+                                           "eager calls vs one HIP graph replay"}
+    log(f"decode step, 1 sequence x 4096 tokens: eager {med_e * 1e6:.1f} us, graph replay {med_g * 1e6:.1f} us")
+    del graph, kq, vq
 
     # the same caches in 16-token pages [P, Hkv, 16, D], scattered over the pool by a random block table
     ps = 16
