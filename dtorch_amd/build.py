@@ -24,7 +24,7 @@ BUILD = os.path.join(ROOT, "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["prefill_fwd.hip", "prefill_f32.hip", "prefill_fp8.hip", "decode_splitkv.hip", "lse_merge.hip", "fp8_quant.hip", "kv_append.hip",
+HIP_SOURCES = ["prefill_fwd.hip", "prefill_f32.hip", "prefill_wide.hip", "prefill_fp8.hip", "decode_splitkv.hip", "lse_merge.hip", "fp8_quant.hip", "kv_append.hip",
                "dtattn_abi.cpp"]
 HOST_SOURCES = ["host/sdpa_op.cc", "host/bindings.cc"]
 

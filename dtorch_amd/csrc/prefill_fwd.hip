@@ -366,7 +366,7 @@ static int dispatch_prefill_m(const PrefillParams& p, int D, bool causal, hipStr
         return causal ? launch_prefill<T, 64, 1, true, MASKED>(p, stream)
                       : launch_prefill<T, 64, 1, false, MASKED>(p, stream);
     }
-    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %d not supported (64 or 128)", D);
+    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %d not supported (64, 128, 256 or 512)", D);
 }
 
 template <typename T>
@@ -377,6 +377,7 @@ static int dispatch_prefill(const PrefillParams& p, int D, bool causal, hipStrea
 
 int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_t stream);
 int prefill_f32(const PrefillParams& p, int D, bool causal, hipStream_t stream);
+int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, hipStream_t stream);
 
 static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
@@ -478,6 +479,7 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     const int D = (int)a->D;
     const bool causal = a->causal != 0;
     if (a->dtype == DTATTN_FP32) return prefill_f32(p, D, causal, stream);
+    if (D == 256 || D == 512) return prefill_wide(p, D, causal, a->dtype == DTATTN_BF16, stream);
     if (a->dtype == DTATTN_BF16) return dispatch_prefill<bf16_t>(p, D, causal, stream);
     return dispatch_prefill<f16_t>(p, D, causal, stream);
 }

@@ -1,0 +1,299 @@
+// Attention forward for wide heads (D = 256, 512) on bf16 / fp16 MFMA, with per-row LSE.
+//
+// The arithmetic of SdpaOp::Compute (dtorch/core/operators/standard/scaled_dot_product_attention_op.cc:
+// 107-109) at head dims where the main kernel's plan (32 query rows per wave, Q and O of the full head
+// in registers) needs more than 512 registers per wave.  The reference reaches it through the VAE
+// mid-block attention of its diffusers ports: one head of block_out_channels[-1] = 512 dimensions
+// (python/dtorch/applications/huggingface/diffusers/models/unets/unet_2d_blocks.py:126-140).
+//
+// Work decomposition: a workgroup owns 32 query rows of one (batch, query head).  Wave w owns the
+// dimensions [w D/4, (w+1) D/4): it holds Q and accumulates O for that quarter only.
+//   - S^T = K Q^T is a sum over the four quarters: each wave computes its partial 32x32 tile with
+//     v_mfma_f32_32x32x16, writes it to LDS, and after one barrier every wave reads and sums all four.
+//     The softmax of the 32x32 tile is then computed identically by the four waves (16 scores per
+//     lane), so no further exchange is needed.
+//   - O^T = V^T P^T for the wave's quarter, with V^T read by ds_read_b64_tr_b16 as in the main kernel.
+// Key tiles of 32 rows, K and V double-buffered through direct buffer->LDS loads: 128 KB plus the 20 KB
+// exchange at D = 512, 84 KB at D = 256; one workgroup per CU either way.
+#include "dtattn_common.hpp"
+#include "prefill_params.hpp"
+
+namespace dtattn {
+
+template <int D>
+__device__ __forceinline__ int wswz(int r) {  // 16-byte chunk swizzle of LDS row r (D >= 128)
+    return 4 * (r & 3) + ((r >> 2) & 3);
+}
+
+template <typename T, int D, bool CAUSAL, bool MASKED>
+__global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParams p) {
+    constexpr int NW = 4;
+    constexpr int BN = 32;           // keys per tile
+    constexpr int BM = 32;           // query rows per workgroup
+    constexpr int DQ = D / NW;       // dimensions per wave
+    constexpr int DCH = D / 8;       // 16-byte chunks per row
+    constexpr int KSTEPS = DQ / 16;  // S^T k-steps per wave
+    constexpr int DT = DQ / 32;      // 32-row d tiles of the wave's O^T
+    constexpr int SXP = 20;          // exchange pitch in floats per lane (16 + 4: conflict-free)
+    static_assert(D == 256 || D == 512, "wide head dims");
+    typedef typename Elem<T>::vec8 V8;
+    typedef typename Elem<T>::vec4 V4;
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+    __shared__ __attribute__((aligned(16))) T Ka[BN * D];
+    __shared__ __attribute__((aligned(16))) T Kb[BN * D];
+    __shared__ __attribute__((aligned(16))) T Va[BN * D];
+    __shared__ __attribute__((aligned(16))) T Vb[BN * D];
+    __shared__ __attribute__((aligned(16))) float Sx[NW * 64 * SXP];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31;
+    const int hf = lane >> 5;
+    const int d0 = wave * DQ;  // first dimension of this wave's quarter
+
+    const BlockCoord bc = block_coord<CAUSAL>(p);
+    const int qb = bc.qb, b = bc.b, hq = bc.hq, hk = bc.hk;
+    const T* qp = reinterpret_cast<const T*>(p.q) + b * p.qs_b + hq * p.qs_h;
+    const T* kp = reinterpret_cast<const T*>(p.k) + b * p.ks_b + hk * p.ks_h;
+    const T* vp = reinterpret_cast<const T*>(p.v) + b * p.vs_b + hk * p.vs_h;
+    const int q0 = qb * BM;
+
+    int kend = p.Sk;
+    if (CAUSAL) {
+        const int lim = q0 + BM + p.delta;  // keys < lim can be visible
+        kend = lim < 0 ? 0 : (lim < p.Sk ? lim : p.Sk);
+    }
+    const int nt = (kend + BN - 1) / BN;
+
+    // Q fragment of the wave's quarter (B operand of S^T): lane holds query l32, d = d0 + ks*16 + hf*8 .. +8.
+    V8 qf[KSTEPS];
+    {
+        const int qrow = q0 + l32;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            u32x4 raw = {0u, 0u, 0u, 0u};
+            if (qrow < p.Sq) raw = ld16(qp + (int64_t)qrow * p.qs_s + d0 + ks * 16 + hf * 8);
+            qf[ks] = __builtin_bit_cast(V8, raw);
+        }
+    }
+    f32x16 oacc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[dt][i] = 0.f;
+    float mrow = kNegInf, lrow = 0.f;
+
+    const int krow = (int)(p.ks_s * (int64_t)sizeof(T));
+    const int vrow = (int)(p.vs_s * (int64_t)sizeof(T));
+
+    // Tile t -> LDS (lane l -> byte 16*l of a 1 KB block, 1024 / (2 D) rows per instruction), chunk c of
+    // row r at c ^ wswz(r); rows past Sk read zeros.
+    auto dma = [&](T* dst, const T* base, int pitch, int64_t stride, int t) {
+        constexpr int ROWS_PER_INSTR = 1024 / (2 * D);
+        constexpr int INSTR = BN / ROWS_PER_INSTR / NW;
+        const int rows = min(BN, p.Sk - t * BN);
+        const auto rs = make_rsrc(base + (int64_t)t * BN * stride, (uint32_t)((rows - 1) * pitch + D * (int)sizeof(T)));
+#pragma unroll
+        for (int i = 0; i < INSTR; ++i) {
+            const int r0 = (wave * INSTR + i) * ROWS_PER_INSTR;
+            const int r = r0 + lane / DCH;
+            const int c = (lane % DCH) ^ wswz<D>(r);
+            buf_ld16_lds_async(rs, dst + r0 * D, (uint32_t)(r * pitch + c * 16));
+        }
+    };
+
+    // V^T reads (ds_read_b64_tr_b16), as in the main kernel: within each 16-lane block, lane 4j+a
+    // addresses key K0+j, d-segment D0+4a.
+    const int blk = lane >> 4, bl = lane & 15;
+    const int tr_key = bl >> 2;
+    const int tr_d = 16 * (blk & 1) + 4 * (bl & 3);
+    const int tr_k4 = 4 * (blk >> 1);
+
+    const float* mbase_p = MASKED ? p.mask + b * p.ms_b + hq * p.ms_h : nullptr;
+    const auto mrs = make_rsrc(mbase_p, MASKED ? (uint32_t)((((int64_t)(p.Sq - 1) * p.ms_l + p.Sk) * 4)) : 0u);
+    const uint32_t mrow_off = MASKED ? (uint32_t)((int64_t)min(q0 + l32, p.Sq - 1) * p.ms_l * 4) : 0u;
+
+    float* sx_mine = Sx + (wave * 64 + lane) * SXP;
+
+    auto tile = [&](const T* Kc, const T* Vc, T* Kn, T* Vn, int t) {
+        wait_vmem();
+        lds_barrier();  // tile t landed; every wave finished tile t-1, including its exchange reads
+        if (t + 1 < nt) {
+            dma(Kn, kp, krow, p.ks_s, t + 1);
+            dma(Vn, vp, vrow, p.vs_s, t + 1);
+        }
+        const int kbase = t * BN;
+        const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && (kbase + BN - 1 > q0 + p.delta));
+        u32x4 mraw[4];
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) mraw[g] = buf_ld16(mrs, mrow_off + (uint32_t)((kbase + 8 * g + 4 * hf) * 4));
+        }
+        // partial S^T over this wave's quarter
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            const int r = l32;
+            const int c = (d0 + ks * 16 + hf * 8) >> 3;
+            const V8 a = *reinterpret_cast<const V8*>(Kc + r * D + 8 * (c ^ wswz<D>(r)));
+            s = Elem<T>::mfma32(a, qf[ks], s);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<f32x4*>(sx_mine + 4 * j) = f32x4{s[4 * j], s[4 * j + 1], s[4 * j + 2], s[4 * j + 3]};
+        lds_barrier();  // all four partials written
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float* src = Sx + (w * 64 + lane) * SXP;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(src + 4 * j);
+                s[4 * j] += x.x, s[4 * j + 1] += x.y, s[4 * j + 2] += x.z, s[4 * j + 3] += x.w;
+            }
+        }
+        // Element i of s holds key kbase + 8*(i/4) + 4*hf + i%4 of query q0 + l32.
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 m = __builtin_bit_cast(f32x4, mraw[g]);
+                s[4 * g + 0] += m.x * p.inv_scale;
+                s[4 * g + 1] += m.y * p.inv_scale;
+                s[4 * g + 2] += m.z * p.inv_scale;
+                s[4 * g + 3] += m.w * p.inv_scale;
+            }
+        }
+        if (need_mask) {
+            int lim = p.Sk - 1 - kbase;
+            if (CAUSAL) lim = min(lim, q0 + l32 + p.delta - kbase);
+            lim -= 4 * hf;
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (8 * (i >> 2) + (i & 3) > lim) s[i] = kNegInf;
+        }
+        float mx = kNegInf;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+        mx = max_xor32(mx);
+        const float mcand = fmaxf(mrow, mx * p.c);
+        if (__any(mcand - mrow > kRescaleThreshold)) {  // wave-uniform (and the same in every wave)
+            const float alpha = fast_exp2(mrow - (mcand == kNegInf ? 0.f : mcand));
+            mrow = mcand;
+            lrow *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+        }
+        const float mbase = (mrow == kNegInf) ? 0.f : mrow;
+        V8 pb[2];
+        float ls = lrow;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            V8 pk;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float pv = fast_exp2(__builtin_fmaf(s[8 * half + e], p.c, -mbase));
+                ls += pv;
+                pk[e] = Elem<T>::from_f32(pv);
+            }
+            pb[half] = pk;
+        }
+        lrow = ls;
+        // O^T (this wave's quarter) += V^T P^T: k-step ks covers keys 16 ks .. 16 ks + 15
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int d = d0 + dt * 32 + tr_d;
+                const int k1 = ks * 16 + tr_k4 + tr_key;
+                const int k2 = k1 + 8;
+                const V4 lo = __builtin_bit_cast(
+                    V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vc + k1 * D + 8 * ((d >> 3) ^ wswz<D>(k1)) + (d & 7))));
+                const V4 hi = __builtin_bit_cast(
+                    V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vc + k2 * D + 8 * ((d >> 3) ^ wswz<D>(k2)) + (d & 7))));
+                const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                oacc[dt] = Elem<T>::mfma32(a, pb[ks], oacc[dt]);
+            }
+        }
+    };
+
+    if (nt > 0) {
+        dma(Ka, kp, krow, p.ks_s, 0);
+        dma(Va, vp, vrow, p.vs_s, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): Q and tile 0, visibly to the compiler
+    for (int t = 0; t < nt; t += 2) {
+        tile(Ka, Va, Kb, Vb, t);
+        if (t + 1 < nt) tile(Kb, Vb, Ka, Va, t + 1);
+    }
+
+    // Epilogue: every wave stages its quarter of the 32 output rows in Ka (row r, 16-byte chunk c at
+    // c ^ (r % 16)), then all 256 threads store whole rows.
+    __syncthreads();
+    {
+        const float l = sum_xor32(lrow);
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        const int row = l32;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                V4 o4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o4[e] = Elem<T>::from_f32(oacc[dt][4 * i4 + e] * inv);
+                const int c = (d0 >> 3) + dt * 4 + i4;
+                *reinterpret_cast<V4*>(Ka + row * D + 8 * (c ^ (row & 15)) + 4 * hf) = o4;
+            }
+        if (wave == 0 && p.lse != nullptr && hf == 0) {
+            const int qrow = q0 + row;
+            if (qrow < p.Sq) p.lse[b * p.lses_b + hq * p.lses_h + qrow] = l > 0.f ? (mrow + __log2f(l)) * kLn2 : kNegInf;
+        }
+    }
+    __syncthreads();
+    T* op = reinterpret_cast<T*>(p.o) + b * p.os_b + hq * p.os_h;
+#pragma unroll
+    for (int it = 0; it < BM * DCH / 256; ++it) {
+        const int id = it * 256 + tid;
+        const int row = id / DCH, c = id % DCH;
+        const int qrow = q0 + row;
+        if (qrow < p.Sq) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Ka + row * D + 8 * (c ^ (row & 15))));
+    }
+}
+
+template <typename T, int D, bool CAUSAL, bool MASKED>
+static int launch_wide(const PrefillParams& prm, hipStream_t stream) {
+    PrefillParams p = prm;
+    p.n_qblocks = (p.Sq + 31) / 32;
+    const int64_t grid = (int64_t)p.n_qblocks * p.B * p.Hq;
+    if (grid == 0) return DTATTN_OK;
+    if (grid > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill grid too large (%lld blocks)", (long long)grid);
+    hipLaunchKernelGGL((prefill_wide_kernel<T, D, CAUSAL, MASKED>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    return check_launch("prefill_wide_kernel");
+}
+
+template <typename T, bool MASKED>
+static int dispatch_wide_m(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
+    if (D == 256)
+        return causal ? launch_wide<T, 256, true, MASKED>(p, stream) : launch_wide<T, 256, false, MASKED>(p, stream);
+    if (D == 512)
+        return causal ? launch_wide<T, 512, true, MASKED>(p, stream) : launch_wide<T, 512, false, MASKED>(p, stream);
+    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %d not supported (64, 128, 256 or 512)", D);
+}
+
+// Entry from dtattn_prefill_fwd for D = 256 / 512 with bf16 or fp16 inputs.
+int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, hipStream_t stream) {
+    if (bf16)
+        return p.mask != nullptr ? dispatch_wide_m<bf16_t, true>(p, D, causal, stream)
+                                 : dispatch_wide_m<bf16_t, false>(p, D, causal, stream);
+    return p.mask != nullptr ? dispatch_wide_m<f16_t, true>(p, D, causal, stream)
+                             : dispatch_wide_m<f16_t, false>(p, D, causal, stream);
+}
+
+}  // namespace dtattn

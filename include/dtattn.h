@@ -53,7 +53,7 @@ typedef enum {
  * dtype: BF16 or FP16 (inputs and output, fp32 softmax and accumulation); FP32 (inputs and output,
  * every step in fp32: the fp32 matrix cores, no 16-bit rounding of P; ABI version 5); or FP8_E4M3FN
  * inputs with descales and a BF16 output.
- * Head dims: D == Dv, D in {64, 128}.
+ * Head dims: D == Dv; D in {64, 128}, and for BF16/FP16 also {256, 512} (ABI version 5).
  */
 typedef struct {
     const void* q; /* [B, Hq, Sq, D] */
