@@ -6,8 +6,8 @@ S=2048, D=128, bf16), inputs resident in HBM.  ``value`` is algorithmic TFLOP/s 
 4*B*Hq*D*S(S+1)/2) over the timed steps.  Also reported, each on its own synthetic inputs: split-KV
 decode HBM GB/s (B=64, Hq=32, Hkv=8, D=128, lengths U[512, 8192]) with a contiguous and a paged cache,
 one decode step (KV-cache append of one token + decode), eager and as a HIP graph replay, the ring step (4 blocks + LSE merge), MMDiT
-joint attention in bf16 and fp8, the small causal MHA case in fp32 and bf16, and fp32 prefill on the
-headline shape.  The CPU baseline is
+joint attention in bf16 and fp8, the VAE attention (one head of 512), the small causal MHA case in fp32
+and bf16, and fp32 prefill on the headline shape.  The CPU baseline is
 libtorch's CPU SDPA in bf16 (the call SdpaOp::Compute makes on a CPU mesh) on the same prefill, timed
 on this host over about ten seconds of repetitions, and compared with the GPU output.
 
@@ -253,6 +253,15 @@ def secondary_workloads(torch, F, dev, timer):
     log(f"MMDiT 1x24x4608: bf16 {f5 / med / 1e12:.0f} TFLOP/s; fp8 end-to-end {f5 / med8 / 1e12:.0f} TFLOP/s "
         f"(quantize {med_q * 1e6:.0f} us, attention ~{f5 / kern8 / 1e12:.0f} TFLOP/s)")
     del q5, k5, v5
+
+    # the VAE mid-block attention of the diffusers ports: 128x128 latent pixels, one head of 512 dims
+    qv5, kv5, vv5 = (torch.randn(1, 1, 16384, 512, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    fv = 4 * 512 * 16384 * 16384
+    med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(qv5, kv5, vv5), reps=5)
+    extras["vae_attention_d512"] = {"TFLOP/s": round(fv / med / 1e12, 1), "frac_bf16": round(fv / med / PEAK_BF16, 4),
+                                    "us": round(med * 1e6, 1)}
+    log(f"VAE attention 1x1x16384 D=512: {fv / med / 1e12:.0f} TFLOP/s")
+    del qv5, kv5, vv5
 
     # the CPU-runnable causal MHA case (B=1, H=8, S=512, D=64) in its own dtype, fp32, and in bf16
     q1, k1, v1 = (torch.randn(1, 8, 512, 64, device=dev, generator=g) for _ in range(3))
