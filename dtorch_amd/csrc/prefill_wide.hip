@@ -20,10 +20,10 @@
 
 namespace dtattn {
 
-template <int D>
-__device__ __forceinline__ int wswz(int r) {  // 16-byte chunk swizzle of LDS row r (D >= 128)
-    return 4 * (r & 3) + ((r >> 2) & 3);
-}
+// 16-byte chunk swizzle of LDS row r: distinct over any 16 consecutive rows (the K reads take one chunk of
+// 16 rows per step) and differing above the low two bits for 4 consecutive rows (a transposed V read
+// takes 4 aligned chunks of 4 rows); rows are whole multiples of 256 bytes, so every row starts on bank 0.
+__device__ __forceinline__ int wswz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
 
 template <typename T, int D, bool CAUSAL, bool MASKED>
 __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParams p) {
@@ -100,7 +100,7 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
         for (int i = 0; i < INSTR; ++i) {
             const int r0 = (wave * INSTR + i) * ROWS_PER_INSTR;
             const int r = r0 + lane / DCH;
-            const int c = (lane % DCH) ^ wswz<D>(r);
+            const int c = (lane % DCH) ^ wswz(r);
             buf_ld16_lds_async(rs, dst + r0 * D, (uint32_t)(r * pitch + c * 16));
         }
     };
@@ -140,7 +140,7 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
         for (int ks = 0; ks < KSTEPS; ++ks) {
             const int r = l32;
             const int c = (d0 + ks * 16 + hf * 8) >> 3;
-            const V8 a = *reinterpret_cast<const V8*>(Kc + r * D + 8 * (c ^ wswz<D>(r)));
+            const V8 a = *reinterpret_cast<const V8*>(Kc + r * D + 8 * (c ^ wswz(r)));
             s = Elem<T>::mfma32(a, qf[ks], s);
         }
 #pragma unroll
@@ -215,9 +215,9 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
                 const int k1 = ks * 16 + tr_k4 + tr_key;
                 const int k2 = k1 + 8;
                 const V4 lo = __builtin_bit_cast(
-                    V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vc + k1 * D + 8 * ((d >> 3) ^ wswz<D>(k1)) + (d & 7))));
+                    V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vc + k1 * D + 8 * ((d >> 3) ^ wswz(k1)) + (d & 7))));
                 const V4 hi = __builtin_bit_cast(
-                    V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vc + k2 * D + 8 * ((d >> 3) ^ wswz<D>(k2)) + (d & 7))));
+                    V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Vc + k2 * D + 8 * ((d >> 3) ^ wswz(k2)) + (d & 7))));
                 const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                 oacc[dt] = Elem<T>::mfma32(a, pb[ks], oacc[dt]);
             }
