@@ -45,11 +45,16 @@ struct DecodeParams {
 
 constexpr int kDecodeChunk = 128;  // smallest split; workspace queries with chunk 0 size for it
 
-// Split length picked for chunk = 0: 256 tokens, or 128 for the 8-head workgroups (8 heads per
-// workgroup leave no registers for 256-token splits).  Measured on one MI355X over batch 1-128,
-// contexts 2K-128K: 256 was best or within 2% for 1-4 heads per workgroup; with 8 heads per
-// workgroup 128 streamed 3.0 TB/s against 2.1-2.3 TB/s.
-static int32_t auto_chunk(int64_t Hq, int64_t Hkv) { return (Hq / Hkv) % 8 == 0 && Hkv % 8 != 0 ? 128 : 256; }
+// Split length picked for chunk = 0: 128 tokens for the 8-head workgroups (8 heads per workgroup
+// leave no registers for longer splits: 3.0 TB/s at 128 against 2.1-2.3 TB/s at 256); 384 for
+// 16-bit rows of 128 (each wave then keeps 48 KB of K/V in flight instead of 32 KB, using the
+// registers that 2 waves per SIMD leave free); 256 otherwise.  Measured on one MI355X over batch
+// 1-128, contexts 2K-128K, 4 heads per workgroup: 384 was 3-8% faster than 256 everywhere except
+// one 8K sequence (-1%); 256 had been best or within 2% of 128 and 512.
+static int32_t auto_chunk(int64_t Hq, int64_t Hkv, int64_t esz, int64_t D) {
+    if ((Hq / Hkv) % 8 == 0 && Hkv % 8 != 0) return 128;
+    return esz == 2 && D == 128 ? 384 : 256;
+}
 
 size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk, int64_t* nsplit_out) {
     const int64_t nsplit = (S_max + chunk - 1) / chunk;
@@ -59,8 +64,8 @@ size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t 
     return ((o_bytes + 255) & ~(size_t)255) + ((lse_bytes + 255) & ~(size_t)255);
 }
 
-// G heads per workgroup, D head dim, TPW tokens per wave (chunk = 4 * TPW, sub-blocks of at most 64
-// tokens per wave; all trip counts are compile-time so each sub-block's loads issue together).
+// G heads per workgroup, D head dim, TPW tokens per wave (chunk = 4 * TPW, in sub-blocks per wave;
+// all trip counts are compile-time so each sub-block's loads issue together).
 // PAGED: rows are addressed through the block table with 64-bit loads of clamped token indices;
 // otherwise through a buffer resource over the chunk's rows.
 template <typename T, int D, int G, int TPW, bool PAGED>
@@ -68,7 +73,10 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk: 8 (bf16, fp16) or 4 (fp32)
     constexpr int LPT = D / EPC;          // lanes per token row
     constexpr int TPI = 64 / LPT;         // tokens per wave-wide load
-    constexpr int SBMAX = 16 * TPI < 64 ? 16 * TPI : 64;  // at most 64 tokens and 16 K + 16 V loads per lane
+    // Sub-blocks of at most 64 tokens and 16 K + 16 V loads per lane; 96-token waves (384-token
+    // splits) of 16-bit rows take one sub-block of 96 (24 + 24 loads per lane at D = 128), fp32 rows
+    // three of 32.
+    constexpr int SBMAX = TPW == 96 ? (EPC == 8 ? 96 : 32) : (16 * TPI < 64 ? 16 * TPI : 64);
     constexpr int SB = TPW < SBMAX ? TPW : SBMAX;
     constexpr int NSB = TPW / SB;         // sub-blocks per wave
     constexpr int NI = SB / TPI;          // K (and V) loads per lane per sub-block
@@ -348,8 +356,9 @@ static int dispatch_chunk(const DecodeParams& p, hipStream_t stream) {
     switch (p.chunk) {
         case 128: return launch_decode<T, D, G, 32, PAGED>(p, stream);
         case 256: return launch_decode<T, D, G, 64, PAGED>(p, stream);
+        case 384: return launch_decode<T, D, G, 96, PAGED>(p, stream);
         case 512: return launch_decode<T, D, G, 128, PAGED>(p, stream);
-        default: return fail(DTATTN_ERR_UNSUPPORTED, "decode: chunk %d not supported (128, 256, 512)", p.chunk);
+        default: return fail(DTATTN_ERR_UNSUPPORTED, "decode: chunk %d not supported (128, 256, 384, 512)", p.chunk);
     }
 }
 
@@ -393,9 +402,9 @@ extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_)
     if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16 && a->dtype != DTATTN_FP32)
         return fail(DTATTN_ERR_UNSUPPORTED, "decode: dtype %d not supported (bf16, fp16, fp32)", a->dtype);
     const int64_t esz = a->dtype == DTATTN_FP32 ? 4 : 2;
-    const int32_t chunk = a->chunk > 0 ? a->chunk : auto_chunk(a->Hq, a->Hkv);
-    if (chunk != 128 && chunk != 256 && chunk != 512)
-        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: chunk %d must be 128, 256 or 512", chunk);
+    const int32_t chunk = a->chunk > 0 ? a->chunk : auto_chunk(a->Hq, a->Hkv, esz, a->D);
+    if (chunk != 128 && chunk != 256 && chunk != 384 && chunk != 512)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: chunk %d must be 128, 256, 384 or 512", chunk);
     // chunk rows are addressed with 32-bit byte offsets
     if (a->k_stride[2] * esz * chunk >= ((int64_t)1 << 31) || a->v_stride[2] * esz * chunk >= ((int64_t)1 << 31))
         return fail(DTATTN_ERR_UNSUPPORTED, "decode: cache row pitch too large");
@@ -469,13 +478,13 @@ extern "C" int dtattn_decode_paged(const dtattn_decode_paged_args* a, void* stre
     if (a->B == 0) return DTATTN_OK;
     if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16 && a->dtype != DTATTN_FP32)
         return fail(DTATTN_ERR_UNSUPPORTED, "decode_paged: dtype %d not supported (bf16, fp16, fp32)", a->dtype);
-    const int32_t chunk = a->chunk > 0 ? a->chunk : auto_chunk(a->Hq, a->Hkv);
-    if (chunk != 128 && chunk != 256 && chunk != 512)
-        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: chunk %d must be 128, 256 or 512", chunk);
+    const int64_t esz = a->dtype == DTATTN_FP32 ? 4 : 2;
+    const int32_t chunk = a->chunk > 0 ? a->chunk : auto_chunk(a->Hq, a->Hkv, esz, a->D);
+    if (chunk != 128 && chunk != 256 && chunk != 384 && chunk != 512)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: chunk %d must be 128, 256, 384 or 512", chunk);
     if (a->q == nullptr || a->k_pages == nullptr || a->v_pages == nullptr || a->block_table == nullptr ||
         a->lengths == nullptr || a->o == nullptr)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: null pointer");
-    const int64_t esz = a->dtype == DTATTN_FP32 ? 4 : 2;
     const int64_t s_all[] = {a->q_stride[0], a->q_stride[1], a->k_stride[0], a->k_stride[1], a->k_stride[2],
                              a->v_stride[0], a->v_stride[1], a->v_stride[2]};
     for (int64_t s : s_all)

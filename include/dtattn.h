@@ -110,8 +110,9 @@ typedef struct {
     int64_t lse_stride[1]; /* B (H stride is 1) */
     int32_t dtype;         /* BF16, FP16 or FP32 (FP32 from ABI version 5) */
     float scale;           /* <= 0 means 1/sqrt(D) */
-    int32_t chunk;         /* tokens per split: 128, 256 or 512; 0 picks 256 (128 when Hq / Hkv is a
-                              multiple of 8 and Hkv is not); workspace sizes for chunk 0 cover it */
+    int32_t chunk;         /* tokens per split: 128, 256, 384 or 512; 0 picks 128 when Hq / Hkv is a
+                              multiple of 8 and Hkv is not, else 384 for bf16/fp16 with D = 128 and
+                              256 otherwise; workspace sizes for chunk 0 cover every choice */
     void* workspace;       /* >= dtattn_decode_workspace_size(...) bytes, 256-byte aligned */
     size_t workspace_bytes;
 } dtattn_decode_args;
@@ -145,7 +146,7 @@ typedef struct {
     int64_t block_table_stride;/* elements between rows of block_table */
     int32_t dtype;             /* BF16, FP16 or FP32 (FP32 from ABI version 5) */
     float scale;               /* <= 0 means 1/sqrt(D) */
-    int32_t chunk;             /* tokens per split: 128, 256 or 512; 0 picks as dtattn_decode_args does */
+    int32_t chunk;             /* tokens per split: 128, 256, 384 or 512; 0 picks as dtattn_decode_args does */
     void* workspace;           /* >= dtattn_decode_paged_workspace_size(...) bytes, 256-byte aligned */
     size_t workspace_bytes;
 } dtattn_decode_paged_args;

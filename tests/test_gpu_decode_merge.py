@@ -39,6 +39,8 @@ def _decode_case(B, Hq, Hkv, Smax, D, lengths, chunk=0, dtype=torch.bfloat16, se
     (2, 64, 8, 600, 128, [600, 257], 0),              # GQA 8 with Hkv 8: two 4-head workgroups per kv head
     (2, 12, 2, 300, 128, [300, 77], 0),               # GQA 6 -> subgroups of 2
     (2, 8, 4, 520, 64, [519, 3], 512),                # D = 64, chunk 512
+    (4, 32, 8, 1200, 128, [383, 384, 385, 1200], 0),  # default 384-token splits: boundaries
+    (2, 8, 4, 800, 64, [769, 384], 384),              # D = 64, chunk 384
 ])
 def test_decode_small(B, Hq, Hkv, Smax, D, lengths, chunk):
     o, lse, ro, rl = _decode_case(B, Hq, Hkv, Smax, D, lengths, chunk)
@@ -59,7 +61,7 @@ def test_decode_split_invariance_and_prefill_equality():
         randn(rng, (B, Hkv, Smax, D)))
     lengths = torch.tensor([900, 450], dtype=torch.int32, device="cuda")
     F = _F()
-    outs = [F.decode_attention(q, kc, vc, lengths, chunk=c) for c in (128, 256, 512)]
+    outs = [F.decode_attention(q, kc, vc, lengths, chunk=c) for c in (128, 256, 384, 512)]
     for o, l in outs[1:]:
         assert max_abs(host(o), host(outs[0][0])) <= O_TOL_BF16
         assert lse_rel(host(l), host(outs[0][1])) <= LSE_TOL

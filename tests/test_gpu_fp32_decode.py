@@ -33,6 +33,7 @@ def _dev(x):
     (2, 64, 8, 600, 128, [600, 0], 0),                 # two 4-head workgroups per kv head; an empty sequence
     (2, 12, 2, 300, 128, [300, 77], 512),              # GQA 6 -> subgroups of 2
     (2, 8, 4, 520, 64, [519, 3], 256),                 # D = 64
+    (3, 8, 2, 1000, 128, [383, 385, 1000], 384),       # 384-token splits: three 32-token sub-blocks per wave
 ])
 def test_decode_fp32(B, Hq, Hkv, Smax, D, lengths, chunk):
     rng = np.random.default_rng(70 + Smax)
