@@ -130,7 +130,10 @@ def test_workspace_sizes():
     lse_bytes = 64 * 32 * nsplit * 4
     up = lambda x: (x + 255) // 256 * 256
     assert n == up(o_bytes) + up(lse_bytes)
-    assert lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 0) == n  # default chunk 128
+    assert lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 0) == n  # sized for the smallest split, 128
+    ns384 = -(-8192 // 384)  # 22 splits of 384 tokens
+    assert lib.dtattn_decode_workspace_size(64, 32, 8192, 128, 384) == up(64 * 32 * ns384 * 128 * 4) + up(
+        64 * 32 * ns384 * 4)
     lib.dtattn_fp8_quantize_workspace_size.restype = ctypes.c_size_t
     lib.dtattn_fp8_quantize_workspace_size.argtypes = [ctypes.c_int64] * 4
     assert lib.dtattn_fp8_quantize_workspace_size(1, 24, 4608, 128) == ((24 * 72 * 4 + 255) // 256) * 256  # 64-row slices
@@ -156,6 +159,10 @@ def test_decode_paged_validation():
     a.Hq = 5  # not a multiple of Hkv
     assert lib.dtattn_decode_paged(ctypes.byref(a), None) == 1 and "multiple" in _last_error()
     a.Hq = 8
+    assert lib.dtattn_decode_paged(ctypes.byref(a), None) == 1 and "null" in _last_error()
+    a.chunk = 640  # split lengths are 128, 256, 384 or 512
+    assert lib.dtattn_decode_paged(ctypes.byref(a), None) == 1 and "chunk" in _last_error()
+    a.chunk = 384  # accepted: validation goes on to the pointers
     assert lib.dtattn_decode_paged(ctypes.byref(a), None) == 1 and "null" in _last_error()
     lib.dtattn_decode_paged_workspace_size.restype = ctypes.c_size_t
     lib.dtattn_decode_paged_workspace_size.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int32]
