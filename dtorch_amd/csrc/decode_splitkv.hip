@@ -47,13 +47,13 @@ constexpr int kDecodeChunk = 128;  // smallest split; workspace queries with chu
 
 // Split length picked for chunk = 0: 128 tokens for the 8-head workgroups (8 heads per workgroup
 // leave no registers for longer splits: 3.0 TB/s at 128 against 2.1-2.3 TB/s at 256); 384 for
-// 16-bit rows of 128 (each wave then keeps 48 KB of K/V in flight instead of 32 KB, using the
-// registers that 2 waves per SIMD leave free); 256 otherwise.  Measured on one MI355X over batch
-// 1-128, contexts 2K-128K, 4 heads per workgroup: 384 was 3-8% faster than 256 everywhere except
-// one 8K sequence (-1%); 256 had been best or within 2% of 128 and 512.
-static int32_t auto_chunk(int64_t Hq, int64_t Hkv, int64_t esz, int64_t D) {
+// 16-bit rows (each wave then keeps 1.5x the K/V bytes in flight of a 256-token split, using the
+// registers that 2 waves per SIMD leave free); 256 for fp32 rows.  Measured on one MI355X over batch
+// 1-128, contexts 2K-128K, 4 heads per workgroup: 384 was 1-8% faster than 256 at D = 64 and 128
+// everywhere except one 8K sequence (-1 to -2%); 256 had been best or within 2% of 128 and 512.
+static int32_t auto_chunk(int64_t Hq, int64_t Hkv, int64_t esz) {
     if ((Hq / Hkv) % 8 == 0 && Hkv % 8 != 0) return 128;
-    return esz == 2 && D == 128 ? 384 : 256;
+    return esz == 2 ? 384 : 256;
 }
 
 size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk, int64_t* nsplit_out) {
@@ -402,7 +402,7 @@ extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_)
     if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16 && a->dtype != DTATTN_FP32)
         return fail(DTATTN_ERR_UNSUPPORTED, "decode: dtype %d not supported (bf16, fp16, fp32)", a->dtype);
     const int64_t esz = a->dtype == DTATTN_FP32 ? 4 : 2;
-    const int32_t chunk = a->chunk > 0 ? a->chunk : auto_chunk(a->Hq, a->Hkv, esz, a->D);
+    const int32_t chunk = a->chunk > 0 ? a->chunk : auto_chunk(a->Hq, a->Hkv, esz);
     if (chunk != 128 && chunk != 256 && chunk != 384 && chunk != 512)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: chunk %d must be 128, 256, 384 or 512", chunk);
     // chunk rows are addressed with 32-bit byte offsets
@@ -479,7 +479,7 @@ extern "C" int dtattn_decode_paged(const dtattn_decode_paged_args* a, void* stre
     if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16 && a->dtype != DTATTN_FP32)
         return fail(DTATTN_ERR_UNSUPPORTED, "decode_paged: dtype %d not supported (bf16, fp16, fp32)", a->dtype);
     const int64_t esz = a->dtype == DTATTN_FP32 ? 4 : 2;
-    const int32_t chunk = a->chunk > 0 ? a->chunk : auto_chunk(a->Hq, a->Hkv, esz, a->D);
+    const int32_t chunk = a->chunk > 0 ? a->chunk : auto_chunk(a->Hq, a->Hkv, esz);
     if (chunk != 128 && chunk != 256 && chunk != 384 && chunk != 512)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_paged: chunk %d must be 128, 256, 384 or 512", chunk);
     if (a->q == nullptr || a->k_pages == nullptr || a->v_pages == nullptr || a->block_table == nullptr ||

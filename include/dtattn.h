@@ -111,8 +111,8 @@ typedef struct {
     int32_t dtype;         /* BF16, FP16 or FP32 (FP32 from ABI version 5) */
     float scale;           /* <= 0 means 1/sqrt(D) */
     int32_t chunk;         /* tokens per split: 128, 256, 384 or 512; 0 picks 128 when Hq / Hkv is a
-                              multiple of 8 and Hkv is not, else 384 for bf16/fp16 with D = 128 and
-                              256 otherwise; workspace sizes for chunk 0 cover every choice */
+                              multiple of 8 and Hkv is not, else 384 for bf16/fp16 and 256 for
+                              fp32; workspace sizes for chunk 0 cover every choice */
     void* workspace;       /* >= dtattn_decode_workspace_size(...) bytes, 256-byte aligned */
     size_t workspace_bytes;
 } dtattn_decode_args;
