@@ -367,8 +367,8 @@ static int dispatch_group(const DecodeParams& p, hipStream_t stream) {
     const int g = p.group;
     // Groups of 8 heads: with Hkv a multiple of 8 the two 4-head subgroups of a kv head have workgroup
     // ids 8 apart, i.e. run on the same XCD, so the second read of each chunk hits that XCD's L2 and
-    // the lighter 4-head kernel takes 256-token splits (measured +5-13% at Hq 64, Hkv 8); otherwise
-    // one 8-head workgroup reads the chunk once.
+    // the lighter 4-head kernel takes the longer default splits of 16-bit rows (measured +5-13% at
+    // Hq 64, Hkv 8); otherwise one 8-head workgroup reads the chunk once (128-token splits).
     if (g % 8 == 0 && p.Hkv % 8 != 0) return dispatch_chunk<T, D, 8, PAGED>(p, stream);
     if (g % 4 == 0) return dispatch_chunk<T, D, 4, PAGED>(p, stream);
     if (g % 2 == 0) return dispatch_chunk<T, D, 2, PAGED>(p, stream);

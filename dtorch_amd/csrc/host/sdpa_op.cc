@@ -52,10 +52,20 @@ struct View4 {
     int64_t sb, sh, ss;
 };
 
-bool Foldable(const at::Tensor& t) {
+// The leading (batch) axes 0 .. nd-4 fold into one axis of stride `sb` iff the axes of size > 1 form
+// one arithmetic progression: for consecutive such axes i < j, stride(i) == stride(j) * size(j).
+// Size-1 axes carry no stride information and are skipped; `sb` is then the stride of the innermost
+// batch axis of size > 1 (any value works when the folded batch is 1, since it is never multiplied
+// by a non-zero index).
+bool FoldBatch(const at::Tensor& t, int64_t& sb) {
     const int64_t nd = t.dim();
-    for (int64_t i = 0; i + 1 <= nd - 4; ++i) {
-        if (t.size(i + 1) != 1 && t.stride(i) != t.stride(i + 1) * t.size(i + 1)) return false;
+    int64_t prev = -1;
+    sb = 0;
+    for (int64_t i = 0; i < nd - 3; ++i) {
+        if (t.size(i) == 1) continue;
+        if (prev >= 0 && t.stride(prev) != t.stride(i) * t.size(i)) return false;
+        prev = i;
+        sb = t.stride(i);
     }
     return true;
 }
@@ -64,14 +74,18 @@ View4 MakeView4(const at::Tensor& in, const char* name) {
     if (in.dim() < 4) Throw(std::string(name) + " must have at least 4 dimensions [..., H, S, D]");
     at::Tensor t = in;
     const int64_t esz = t.element_size();
+    int64_t sb = 0;
     auto ok = [&](const at::Tensor& x) {
-        if (x.stride(-1) != 1 || !Foldable(x)) return false;
+        if (x.stride(-1) != 1 || !FoldBatch(x, sb)) return false;
         if ((reinterpret_cast<uintptr_t>(x.data_ptr()) & 15u) != 0) return false;
         for (int64_t i = 0; i < x.dim() - 1; ++i)
             if (x.size(i) > 1 && (x.stride(i) * esz) % 16 != 0) return false;
         return true;
     };
-    if (!ok(t)) t = t.contiguous();
+    if (!ok(t)) {
+        t = t.contiguous();
+        FoldBatch(t, sb);  // always foldable once contiguous
+    }
     View4 v;
     v.t = t;
     const int64_t nd = t.dim();
@@ -80,13 +94,23 @@ View4 MakeView4(const at::Tensor& in, const char* name) {
     v.H = t.size(nd - 3);
     v.S = t.size(nd - 2);
     v.D = t.size(nd - 1);
-    v.sb = nd > 3 ? t.stride(nd - 4) : 0;
-    if (nd > 3 && t.size(nd - 4) == 1) v.sb = v.H * t.stride(nd - 3);
-    v.sh = t.stride(nd - 3);
-    v.ss = t.stride(nd - 2);
-    if (v.H == 1) v.sh = v.S * v.ss;
+    // Size-1 axes are never indexed past 0, so their strides are free: give them the contiguous
+    // values, which keeps every stride the kernels see a multiple of 16 bytes.
+    v.ss = v.S > 1 ? t.stride(nd - 2) : v.D;
+    v.sh = v.H > 1 ? t.stride(nd - 3) : v.S * v.ss;
+    // A folded batch of 1 is never indexed past 0: give it the extent of one (H, S, D) slab.
+    v.sb = v.B > 1 ? sb : v.H * v.sh;
     return v;
 }
+
+}  // namespace
+
+FoldedView FoldedStrides(const at::Tensor& t) {
+    const View4 v = MakeView4(t, "tensor");
+    return {v.B, v.H, v.S, v.D, v.sb, v.sh, v.ss, !v.t.is_same(t)};
+}
+
+namespace {
 
 void CheckDevice(const std::vector<const at::Tensor*>& ts) {
     const at::Device dev = ts[0]->device();
@@ -156,6 +180,7 @@ PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::T
     if (q_.size(-1) != k_.size(-1)) Throw("query and key head dims differ");
     if (k_.size(-2) != v_.size(-2) || k_.size(-3) != v_.size(-3)) Throw("key and value shapes differ");
     const int64_t hq = q_.size(-3), hkv = k_.size(-3);
+    if (hkv == 0 && hq > 0) Throw("key and value must have at least one head");
     if (hq != hkv) {
         if (!prm.enableGqa) Throw("query and key/value head counts differ; set enable_gqa=True");
         if (hq % hkv != 0) Throw("number of query heads must be a multiple of key/value heads");
@@ -319,7 +344,7 @@ void SdpaWithLseOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray&
     if (!inputs[0].has_value() || !inputs[1].has_value() || !inputs[2].has_value())
         Throw("query, key and value are required");
     const at::Tensor* mask = inputs[3].has_value() && inputs[3]->defined() ? &*inputs[3] : nullptr;
-    PrefillResult r = RunPrefill(*inputs[0], *inputs[1], *inputs[2], mParam, mQOffset, mKOffset, true, mask);
+    PrefillResult r = RunPrefill(*inputs[0], *inputs[1], *inputs[2], mParam, mLseParam.qOffset, mLseParam.kOffset, true, mask);
     outputs.push_back(r.o);
     outputs.push_back(r.lse);
 }
@@ -334,13 +359,13 @@ void SdpaDecodeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& 
     if (q.size(2) != 1) Throw("decode query must have one token per sequence ([B, Hq, 1, D])");
     if (kc.sizes() != vc.sizes()) Throw("k_cache and v_cache shapes differ");
     if (q.size(0) != kc.size(0) || q.size(3) != kc.size(3)) Throw("query and cache shapes do not match");
-    if (q.size(1) % kc.size(1) != 0) Throw("number of query heads must be a multiple of kv heads");
+    if (kc.size(1) <= 0 || q.size(1) % kc.size(1) != 0) Throw("number of query heads must be a multiple of kv heads");
     if (len.scalar_type() != at::kInt || len.dim() != 1 || len.size(0) != q.size(0))
         Throw("lengths must be an int32 tensor of shape [B]");
     const c10::ScalarType st = q.scalar_type();
     if (kc.scalar_type() != st || vc.scalar_type() != st) Throw("query and cache dtypes differ");
     if (st != at::kBFloat16 && st != at::kHalf && st != at::kFloat) Throw("decode supports bf16, fp16 and fp32");
-    if (mScale.has_value() && !(mScale.value() > 0.0)) Throw("scale must be positive");
+    if (mParam.scale.has_value() && !(mParam.scale.value() > 0.0)) Throw("scale must be positive");
 
     at::Tensor o = at::empty(q.sizes(), q.options());
     at::Tensor lse = at::empty({q.size(0), q.size(1)}, q.options().dtype(at::kFloat));
@@ -363,8 +388,8 @@ void SdpaDecodeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& 
     a.o_stride[0] = q.size(1) * q.size(3), a.o_stride[1] = q.size(3);
     a.lse_stride[0] = q.size(1);
     a.dtype = DtypeCode(st);
-    a.scale = mScale.has_value() ? (float)mScale.value() : 0.f;
-    a.chunk = mChunk;
+    a.scale = mParam.scale.has_value() ? (float)mParam.scale.value() : 0.f;
+    a.chunk = mParam.chunk;
     const size_t ws = dtattn_decode_workspace_size(a.B, a.Hq, a.S_max, a.D, a.chunk);
     at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, q.options().dtype(at::kByte));
     a.workspace = wst.data_ptr();
@@ -495,7 +520,7 @@ void SdpaDecodePagedOp::Compute(const TorchTensorOptArray& inputs, TorchTensorAr
     const c10::ScalarType st = q.scalar_type();
     if (kp.scalar_type() != st || vp.scalar_type() != st) Throw("query and page dtypes differ");
     if (st != at::kBFloat16 && st != at::kHalf && st != at::kFloat) Throw("decode supports bf16, fp16 and fp32");
-    if (mScale.has_value() && !(mScale.value() > 0.0)) Throw("scale must be positive");
+    if (mParam.scale.has_value() && !(mParam.scale.value() > 0.0)) Throw("scale must be positive");
     if (kp.stride(3) != 1 || vp.stride(3) != 1) Throw("page pools need a unit stride along D");
 
     at::Tensor o = at::empty(q.sizes(), q.options());
@@ -523,8 +548,8 @@ void SdpaDecodePagedOp::Compute(const TorchTensorOptArray& inputs, TorchTensorAr
     a.lse_stride[0] = q.size(1);
     a.block_table_stride = btc.stride(0);
     a.dtype = DtypeCode(st);
-    a.scale = mScale.has_value() ? (float)mScale.value() : 0.f;
-    a.chunk = mChunk;
+    a.scale = mParam.scale.has_value() ? (float)mParam.scale.value() : 0.f;
+    a.chunk = mParam.chunk;
     const size_t ws = dtattn_decode_paged_workspace_size(a.B, a.Hq, a.max_pages, a.page_size, a.D, a.chunk);
     at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, q.options().dtype(at::kByte));
     a.workspace = wst.data_ptr();
@@ -565,8 +590,15 @@ void LseMergeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& ou
             for (auto& v : os) v = MakeView4(v.t.contiguous(), "O block");
             break;
         }
-    const c10::ScalarType ost = mOutDtype.value_or(st);
-    if (ost != at::kBFloat16 && ost != at::kHalf && ost != at::kFloat) Throw("merge output must be bf16, fp16 or fp32");
+    c10::ScalarType ost = st;
+    if (mParam.outKind.has_value()) {
+        switch (*mParam.outKind) {
+            case DTATTN_BF16: ost = at::kBFloat16; break;
+            case DTATTN_FP16: ost = at::kHalf; break;
+            case DTATTN_FP32: ost = at::kFloat; break;
+            default: Throw("merge output must be bf16, fp16 or fp32");
+        }
+    }
     at::Tensor o = at::empty(o0.sizes(), o0.options().dtype(ost));
     std::vector<int64_t> ls(o0.sizes().begin(), o0.sizes().end() - 1);
     at::Tensor lse = at::empty(ls, o0.options().dtype(at::kFloat));
@@ -595,6 +627,14 @@ void LseMergeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& ou
     Check(dtattn_lse_merge(&a, CurrentStream(o0)), "dtattn_lse_merge");
     outputs.push_back(o);
     outputs.push_back(lse);
+}
+
+LseMergeParam LseMergeOp::ParamFor(std::optional<c10::ScalarType> outDtype) {
+    if (!outDtype.has_value()) return LseMergeParam();
+    const int32_t code = DtypeCode(*outDtype);
+    if (code != DTATTN_BF16 && code != DTATTN_FP16 && code != DTATTN_FP32)
+        Throw("merge output must be bf16, fp16 or fp32");
+    return LseMergeParam(code);
 }
 
 void Fp8QuantizeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const {

@@ -21,6 +21,8 @@
 #include <string>
 #include <vector>
 
+#include "param_archive.h"
+
 namespace dtorch_amd {
 namespace core {
 
@@ -36,9 +38,21 @@ struct SdpaOption {
     std::string sageAttentionType;
     SdpaOption() : sageAttentionType("") {}
     explicit SdpaOption(std::string t) : sageAttentionType(std::move(t)) {}
+
+    template <class Archive>
+    void serialize(Archive& ar, const unsigned int /*version*/) {
+        ar & sageAttentionType;
+    }
 };
 
-// dtorch/core/operators/standard/scaled_dot_product_attention_op.h:14-36 (same fields, same defaults).
+// Operator params.  Each is default-constructible and serialises its fields in declaration order
+// through a boost-style `serialize` member, as the reference's params do
+// (dtorch/core/operators/operator_param.h:19-69 registers the types, operator_serialization_pack.h:91-140
+// dispatches them).  In a DTorch tree each derives from OpParam and serialises
+// `BaseObject<OpParam>(*this)` first; the fields after that are exactly the ones below.
+
+// dtorch/core/operators/standard/scaled_dot_product_attention_op.h:14-36 (same fields, same defaults,
+// same serialisation order).
 struct SdpaParam {
     bool isCausal = false;
     std::optional<double> scale = std::nullopt;
@@ -48,7 +62,74 @@ struct SdpaParam {
     SdpaParam() = default;
     SdpaParam(bool isCausal_, std::optional<double> scale_, bool enableGqa_, std::optional<SdpaOption> option_)
         : isCausal(isCausal_), scale(scale_), enableGqa(enableGqa_), option(std::move(option_)) {}
+
+    template <class Archive>
+    void serialize(Archive& ar, const unsigned int /*version*/) {
+        ar & isCausal;
+        ar & scale;
+        ar & enableGqa;
+        ar & option;
+    }
 };
+
+// SdpaWithLse: the SdpaParam fields, then the causal offsets of a ring block (key j is visible to
+// query i iff j + kOffset <= i + qOffset).  New operator type; no reference counterpart.
+struct SdpaWithLseParam : SdpaParam {
+    int64_t qOffset = 0;
+    int64_t kOffset = 0;
+
+    SdpaWithLseParam() = default;
+    SdpaWithLseParam(SdpaParam base, int64_t qOffset_, int64_t kOffset_)
+        : SdpaParam(std::move(base)), qOffset(qOffset_), kOffset(kOffset_) {}
+
+    template <class Archive>
+    void serialize(Archive& ar, const unsigned int version) {
+        SdpaParam::serialize(ar, version);
+        ar & qOffset;
+        ar & kOffset;
+    }
+};
+
+// SdpaDecode / SdpaDecodePaged: softmax scale (none: 1/sqrt(D)) and tokens per split (0: automatic).
+struct SdpaDecodeParam {
+    std::optional<double> scale = std::nullopt;
+    int32_t chunk = 0;
+
+    SdpaDecodeParam() = default;
+    SdpaDecodeParam(std::optional<double> scale_, int32_t chunk_) : scale(scale_), chunk(chunk_) {}
+
+    template <class Archive>
+    void serialize(Archive& ar, const unsigned int /*version*/) {
+        ar & scale;
+        ar & chunk;
+    }
+};
+struct SdpaDecodePagedParam : SdpaDecodeParam {
+    using SdpaDecodeParam::SdpaDecodeParam;
+    SdpaDecodePagedParam() = default;
+};
+
+// LseMerge: output element type as a dtattn_dtype code (BF16 0, FP16 1, FP32 3); none keeps the
+// blocks' type.
+struct LseMergeParam {
+    std::optional<int32_t> outKind = std::nullopt;
+
+    LseMergeParam() = default;
+    explicit LseMergeParam(std::optional<int32_t> outKind_) : outKind(outKind_) {}
+
+    template <class Archive>
+    void serialize(Archive& ar, const unsigned int /*version*/) {
+        ar & outKind;
+    }
+};
+
+// Operators without knobs still get a param type, as every DTorch operator does.
+struct KvCacheAppendParam {
+    template <class Archive>
+    void serialize(Archive&, const unsigned int) {}
+};
+struct KvCacheAppendPagedParam : KvCacheAppendParam {};
+struct Fp8QuantizeParam : KvCacheAppendParam {};
 
 // One allowed input->output placement assignment for one mesh dimension.  Placements are written
 // "S(i)" (shard on tensor dim i), "R" (replicate); an empty string in `inputs` marks an optional input.
@@ -92,23 +173,26 @@ protected:
 // j + kOffset <= i + qOffset when causal.
 class SdpaWithLseOp : public SdpaOp {
 public:
+    explicit SdpaWithLseOp(SdpaWithLseParam param) : SdpaOp(param), mLseParam(std::move(param)) {}
     SdpaWithLseOp(SdpaParam param, int64_t qOffset, int64_t kOffset)
-        : SdpaOp(std::move(param)), mQOffset(qOffset), mKOffset(kOffset) {}
+        : SdpaWithLseOp(SdpaWithLseParam(std::move(param), qOffset, kOffset)) {}
+    const SdpaWithLseParam& LseParam() const { return mLseParam; }
     void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const override;
 
 private:
-    int64_t mQOffset, mKOffset;
+    SdpaWithLseParam mLseParam;
 };
 
 // {q[B,Hq,1,D], k_cache[B,Hkv,S,D], v_cache[B,Hkv,S,D], lengths[B] int32} -> {O[B,Hq,1,D], LSE[B,Hq]}
 class SdpaDecodeOp {
 public:
-    SdpaDecodeOp(std::optional<double> scale, int32_t chunk) : mScale(scale), mChunk(chunk) {}
+    explicit SdpaDecodeOp(SdpaDecodeParam param) : mParam(std::move(param)) {}
+    SdpaDecodeOp(std::optional<double> scale, int32_t chunk) : mParam(scale, chunk) {}
+    const SdpaDecodeParam& Param() const { return mParam; }
     void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
 
 private:
-    std::optional<double> mScale;
-    int32_t mChunk;
+    SdpaDecodeParam mParam;
 };
 
 // {q[B,Hq,1,D], k_pages[P,Hkv,page,D], v_pages[P,Hkv,page,D], block_table[B,max_pages] int32,
@@ -116,12 +200,13 @@ private:
 // (page, kv head, row within the page, D) with a unit D stride (e.g. a permuted [P,page,Hkv,D] pool).
 class SdpaDecodePagedOp {
 public:
-    SdpaDecodePagedOp(std::optional<double> scale, int32_t chunk) : mScale(scale), mChunk(chunk) {}
+    explicit SdpaDecodePagedOp(SdpaDecodePagedParam param) : mParam(std::move(param)) {}
+    SdpaDecodePagedOp(std::optional<double> scale, int32_t chunk) : mParam(scale, chunk) {}
+    const SdpaDecodePagedParam& Param() const { return mParam; }
     void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
 
 private:
-    std::optional<double> mScale;
-    int32_t mChunk;
+    SdpaDecodePagedParam mParam;
 };
 
 // KV-cache append (no counterpart in the reference: its Llama port keeps no cache,
@@ -143,11 +228,14 @@ public:
 // {O_0, LSE_0, O_1, LSE_1, ...} -> {O, LSE}; O in `outDtype` (default: the blocks' dtype).
 class LseMergeOp {
 public:
-    explicit LseMergeOp(std::optional<c10::ScalarType> outDtype = std::nullopt) : mOutDtype(outDtype) {}
+    explicit LseMergeOp(LseMergeParam param = LseMergeParam()) : mParam(std::move(param)) {}
+    // Convenience: the output type as a torch dtype (bf16, fp16 or fp32).
+    static LseMergeParam ParamFor(std::optional<c10::ScalarType> outDtype);
+    const LseMergeParam& Param() const { return mParam; }
     void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
 
 private:
-    std::optional<c10::ScalarType> mOutDtype;
+    LseMergeParam mParam;
 };
 
 // {x[B,H,S,D]} -> {codes[B,H,S,D] float8_e4m3fn, descale[B,H] fp32}
@@ -155,6 +243,15 @@ class Fp8QuantizeOp {
 public:
     void Compute(const TorchTensorOptArray& inputs, TorchTensorArray& outputs) const;
 };
+
+// How the host operators hand a tensor to the kernels: leading axes folded into one batch axis,
+// element strides of (batch, H, S) and whether a layout copy was needed first.  Exposed for tests.
+struct FoldedView {
+    int64_t B, H, S, D;
+    int64_t sb, sh, ss;
+    bool copied;
+};
+FoldedView FoldedStrides(const at::Tensor& t);
 
 // MI355X peak table of the current device (native analog of DevicePeakPerformance).
 struct DevicePeaks {

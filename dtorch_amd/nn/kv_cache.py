@@ -59,6 +59,18 @@ class KVCache:
         self.append(k_new, v_new)
         return F.decode_attention(q, self.k, self.v, self.lengths, scale=self.scale)[0]
 
+    def sync_lengths(self) -> np.ndarray:
+        """Refresh the host copy of the lengths from the device (one synchronising copy).
+
+        A decode step captured in a HIP graph advances the host copy once, at capture; every replay
+        advances only the device lengths.  Call this after replays and before eager use, so that the
+        capacity check sees the true lengths.  The caller bounds the number of replays by
+        capacity - current length: the append kernel drops tokens past the capacity (and the lengths
+        saturate there), so later replays would attend over a truncated cache.
+        """
+        self._host_len = self.lengths.to("cpu", torch.int64).numpy().copy()
+        return self._host_len.copy()
+
 
 class PagedKVCache:
     """Paged cache: pools [num_pages, Hkv, page_size, D], a block table [B, max_pages] and lengths [B].
@@ -108,3 +120,16 @@ class PagedKVCache:
     def decode(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> torch.Tensor:
         self.append(k_new, v_new)
         return F.decode_attention_paged(q, self.k, self.v, self.block_table, self.lengths, scale=self.scale)[0]
+
+    def sync_lengths(self) -> np.ndarray:
+        """Refresh the host copy of the lengths from the device after HIP-graph replays.
+
+        Replays assign no pages: the block-table slots past a sequence's assigned pages hold page 0, so
+        the caller bounds the replays by the tokens left on the pages already assigned.  Raises if a
+        replay went past them (those tokens were written into page 0).
+        """
+        dev = self.lengths.to("cpu", torch.int64).numpy().copy()
+        if np.any(dev > self._pages * self.page_size):
+            raise RuntimeError("PagedKVCache: graph replays appended past the assigned pages")
+        self._host_len = dev
+        return dev.copy()

@@ -314,3 +314,140 @@ def test_front_end_option_validation():
         F.scaled_dot_product_attention(x, x, x, sdpa_option=F.SdpaOption(sage_attn_type="auto"))
     with pytest.raises(NotImplementedError):
         F.scaled_dot_product_attention(x, x, x, sdpa_option=F.SdpaOption(ring_cp_dim=2))
+
+
+def test_every_param_type_round_trips_in_field_order():
+    import struct
+    base = host.SdpaParam(True, 0.125, False, host.SdpaOption("native_fp8"))
+    # SdpaParam: isCausal, scale, enableGqa, option (scaled_dot_product_attention_op.h:27-35); an optional
+    # is a presence byte plus the value, a string a u64 length plus its bytes.
+    want = (struct.pack("<?", True) + struct.pack("<B", 1) + struct.pack("<d", 0.125) + struct.pack("<?", False) +
+            struct.pack("<B", 1) + struct.pack("<Q", 10) + b"native_fp8")
+    assert base.to_bytes() == want
+    assert host.SdpaParam().to_bytes() == b"\x00\x00\x00\x00"
+    lp = host.SdpaWithLseParam(base, 4096, -7)
+    assert lp.to_bytes() == want + struct.pack("<qq", 4096, -7)
+    cases = [
+        (host.SdpaParam, base, lambda p: (p.is_causal, p.scale, p.enable_gqa, p.option.sage_attention_type)),
+        (host.SdpaWithLseParam, lp, lambda p: (p.is_causal, p.scale, p.q_offset, p.k_offset)),
+        (host.SdpaDecodeParam, host.SdpaDecodeParam(0.09, 384), lambda p: (p.scale, p.chunk)),
+        (host.SdpaDecodeParam, host.SdpaDecodeParam(), lambda p: (p.scale, p.chunk)),
+        (host.SdpaDecodePagedParam, host.SdpaDecodePagedParam(None, 256), lambda p: (p.scale, p.chunk)),
+        (host.LseMergeParam, host.LseMergeParam(3), lambda p: p.out_kind),
+        (host.LseMergeParam, host.LseMergeParam(), lambda p: p.out_kind),
+        (host.KvCacheAppendParam, host.KvCacheAppendParam(), lambda p: type(p).__name__),
+        (host.KvCacheAppendPagedParam, host.KvCacheAppendPagedParam(), lambda p: type(p).__name__),
+        (host.Fp8QuantizeParam, host.Fp8QuantizeParam(), lambda p: type(p).__name__),
+    ]
+    for cls, p, key in cases:
+        q = cls.from_bytes(p.to_bytes())
+        assert key(q) == key(p), cls
+        r = pickle.loads(pickle.dumps(p))
+        assert type(r) is cls and key(r) == key(p), cls
+        assert cls().to_bytes() == cls.from_bytes(cls().to_bytes()).to_bytes()  # default-constructible
+    assert host.SdpaDecodeParam(0.09, 384).to_bytes() == struct.pack("<Bd", 1, 0.09) + struct.pack("<i", 384)
+    assert host.LseMergeParam(3).to_bytes() == struct.pack("<Bi", 1, 3)
+    # a layout mismatch fails loudly instead of leaving fields unset
+    with pytest.raises(ValueError, match="trailing"):
+        host.SdpaParam.from_bytes(lp.to_bytes())
+    with pytest.raises(ValueError, match="truncated"):
+        host.SdpaWithLseParam.from_bytes(base.to_bytes())
+    # the operators keep their params
+    assert host.SdpaWithLseOp(lp).lse_param.q_offset == 4096
+    assert host.SdpaDecodeOp(host.SdpaDecodeParam(None, 128)).param.chunk == 128
+    assert host.LseMergeOp(torch.float32).param.out_kind == 3
+    assert host.LseMergeOp().param.out_kind is None
+
+
+def _element_offset(t, idx):
+    return sum(i * s for i, s in zip(idx, t.stride()))
+
+
+def _check_folded(t):
+    """Every element (b..., h, s, d) of t sits at b*sb + h*sh + s*ss + d of the view the kernels get."""
+    import itertools
+    f = host.folded_strides(t)
+    src = t.contiguous() if f.copied else t
+    batch = t.shape[:-3]
+    assert f.B == int(torch.tensor(batch).prod()) if batch else f.B == 1
+    assert (f.H, f.S, f.D) == tuple(t.shape[-3:])
+    for bi, bidx in enumerate(itertools.product(*[range(n) for n in batch])):
+        for h in {0, t.shape[-3] - 1}:
+            for s in {0, t.shape[-2] - 1}:
+                want = _element_offset(src, (*bidx, h, s, 0))
+                assert bi * f.sb + h * f.sh + s * f.ss == want, (tuple(t.shape), t.stride(), bidx, h, s)
+    for st, n in ((f.sb, f.B), (f.sh, f.H), (f.ss, f.S)):
+        assert (st * t.element_size()) % 16 == 0 or n == 1
+
+
+def test_folded_strides_of_rank5_views():
+    # x.transpose(1, 2).unsqueeze(1): a size-1 axis right before H with a real batch axis before it
+    x = torch.zeros(2, 96, 4, 128, dtype=torch.bfloat16)
+    t = x.transpose(1, 2).unsqueeze(1)
+    f = host.folded_strides(t)
+    assert (f.B, f.sb, f.sh, f.ss, f.copied) == (2, 49152, 128, 512, False)
+    _check_folded(t)
+    # a head slice of a [A, 1, 2H, S, D] tensor
+    y = torch.zeros(2, 1, 8, 16, 64, dtype=torch.bfloat16)[:, :, :4]
+    f = host.folded_strides(y)
+    assert (f.B, f.sb, f.copied) == (2, 8192, False)
+    _check_folded(y)
+    for shape in ((1, 3, 4, 16, 64), (3, 1, 1, 4, 16, 64), (1, 1, 4, 16, 64), (2, 3, 4, 16, 64)):
+        _check_folded(torch.zeros(shape, dtype=torch.bfloat16))
+
+
+def test_folded_strides_property_over_random_views():
+    g = torch.Generator().manual_seed(0)
+    for trial in range(200):
+        nd = int(torch.randint(4, 7, (1,), generator=g))
+        shape = [int(torch.randint(1, 4, (1,), generator=g)) for _ in range(nd - 3)] + [3, 5, 64]
+        base = torch.zeros([n * 2 for n in shape[:-1]] + [64], dtype=torch.bfloat16)
+        t = base[tuple(slice(0, n) for n in shape)]                       # strided slice
+        if trial % 3 == 0 and nd >= 5:
+            t = t.transpose(0, 1)                                        # permuted batch axes
+        if trial % 4 == 1:
+            t = t.transpose(-3, -2).contiguous().transpose(-3, -2)        # [.., S, H, D] memory
+        if trial % 5 == 2:
+            t = t.unsqueeze(int(torch.randint(0, t.dim() - 2, (1,), generator=g)))
+        _check_folded(t)
+
+
+def test_last_error_is_per_thread():
+    # Each thread sees only the message of its own last failing call (validation runs before any device
+    # work, so this needs no GPU).
+    import threading
+    lib.dtattn_last_error.restype = ctypes.c_char_p
+    lib.dtattn_prefill_fwd.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.dtattn_lse_merge.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.dtattn_decode_splitkv.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    calls = {"prefill": (lib.dtattn_prefill_fwd, b"prefill: args is NULL"),
+             "merge": (lib.dtattn_lse_merge, b"merge"),
+             "decode": (lib.dtattn_decode_splitkv, b"decode: args is NULL")}
+    bad, start = [], threading.Barrier(len(calls) + 1)
+
+    def worker(name):
+        fn, want = calls[name]
+        start.wait()
+        for _ in range(2000):
+            if fn(None, None) == 0:
+                bad.append((name, "accepted NULL"))
+                return
+            msg = lib.dtattn_last_error()
+            if want not in msg or any(w in msg for n, (_, w) in calls.items() if n != name):
+                bad.append((name, msg))
+                return
+
+    def quiet():  # never fails a call: its message stays empty throughout
+        start.wait()
+        for _ in range(2000):
+            lib.dtattn_abi_version()
+            if lib.dtattn_last_error() != b"":
+                bad.append(("quiet", lib.dtattn_last_error()))
+                return
+
+    threads = [threading.Thread(target=worker, args=(n,)) for n in calls] + [threading.Thread(target=quiet)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not bad, bad
