@@ -8,13 +8,16 @@ decode HBM GB/s (B=64, Hq=32, Hkv=8, D=128, lengths U[512, 8192]) with a contigu
 one decode step (KV-cache append of one token + decode), eager and as a HIP graph replay, the ring step (4 blocks + LSE merge), MMDiT
 joint attention in bf16 and fp8, the VAE attention (one head of 512), the small causal MHA case in fp32
 and bf16, and fp32 prefill on the headline shape.  The CPU baseline is
-libtorch's CPU SDPA in bf16 (the call SdpaOp::Compute makes on a CPU mesh) on the same prefill, timed
-on this host over about ten seconds of repetitions, and compared with the GPU output.
+libtorch's CPU SDPA (the call SdpaOp::Compute makes on a CPU mesh) on the same prefill, in fp32 on the
+bf16-rounded inputs (and in bf16 beside it), timed on this host over about ten seconds of repetitions,
+and compared with the GPU output.
 
-Order: CPU baseline, secondary workloads, then the headline (W warmup steps, K timed steps).  The
-GPU's clocks need some 30 ms of sustained load to settle after idling (measured: back-to-back prefill
-launches rise from ~610 to ~925 TFLOP/s over the first 30 ms), so the headline runs last, after GPU
-work, and every secondary measurement first runs its workload for 0.15 s untimed.
+Order: CPU baseline, secondary workloads, then the headline (W warmup steps, extended to at least
+0.25 s of launches, then K timed steps).  The GPU's clocks need some 30 ms of sustained load to settle
+after idling (measured: back-to-back prefill launches rise from ~610 to ~925 TFLOP/s over the first
+30 ms), so the headline warm-up is time-based and every secondary measurement first runs its workload
+for 0.15 s untimed.  The CPU baseline also times the decode workload (per-sequence libtorch CPU SDPA)
+right after the GPU decode measurement, on the same cache values.
 
 Prints ONE JSON line on stdout; human-readable detail goes to stderr.
 """
@@ -35,6 +38,7 @@ PEAK_BF16 = 2.5e15   # MI355X dense bf16 MFMA, FLOP/s (published)
 PEAK_FP8 = 5.0e15    # MI355X dense fp8 MFMA
 PEAK_HBM = 8.0e12    # MI355X HBM3E, B/s
 PEAK_FP32 = 157.3e12  # MI355X dense fp32 MFMA
+HEADLINE_SETTLE_S = 0.25  # minimum untimed back-to-back headline launches before the timed steps
 
 # HBM bytes per launch of the headline kernel, from the two calibrated rocprofv3 --pmc runs
 # (FETCH_SIZE, WRITE_SIZE) summarised in this file.
@@ -88,32 +92,71 @@ class Timer:
         return float(np.median(times)), float(np.mean(times))
 
 
+def _timed_reps(fn, min_seconds, min_reps=3):
+    fn()  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while reps < min_reps or time.perf_counter() - t0 < min_seconds:
+        fn()
+        reps += 1
+    return reps, time.perf_counter() - t0
+
+
 def cpu_baseline(torch, qn, kn, vn, min_seconds):
-    """libtorch CPU SDPA (bf16, all threads) on the full headline workload, repeated for min_seconds."""
+    """libtorch CPU SDPA (all threads) on the full headline workload: in fp32 on the bf16-rounded inputs
+    (the reported value), and in bf16 (the same call on the bf16 tensors themselves)."""
     from oracle import dtorch_cpu_path as cpu
 
     threads = torch.get_num_threads()
-    q, k, v = (torch.from_numpy(x).to(torch.bfloat16) for x in (qn, kn, vn))
+    qb, kb, vb = (torch.from_numpy(x).to(torch.bfloat16) for x in (qn, kn, vn))
+    q, k, v = (x.float() for x in (qb, kb, vb))
     B, Hq, S, D = q.shape
-    out = cpu.sdpa(q, k, v, is_causal=True, enable_gqa=True)  # warm-up, and the reference output
-    reps, t0 = 0, time.perf_counter()
-    while reps < 3 or time.perf_counter() - t0 < min_seconds:
-        cpu.sdpa(q, k, v, is_causal=True, enable_gqa=True)
-        reps += 1
-    dt = time.perf_counter() - t0
-    rate = causal_flops(B, Hq, S, D) * reps / dt
+    flops = causal_flops(B, Hq, S, D)
+    out = cpu.sdpa(q, k, v, is_causal=True, enable_gqa=True)  # the reference output for the GPU check
+    reps, dt = _timed_reps(lambda: cpu.sdpa(q, k, v, is_causal=True, enable_gqa=True), min_seconds)
+    rate = flops * reps / dt
+    reps_b, dt_b = _timed_reps(lambda: cpu.sdpa(qb, kb, vb, is_causal=True, enable_gqa=True), min_seconds / 2)
+    rate_b = flops * reps_b / dt_b
     info = {
         "value": round(rate / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
-        "sample": f"libtorch CPU SDPA in bf16 (SdpaOp::Compute's call on a CPU mesh) on the whole workload "
-                  f"(B={B}, Hq={Hq}, Hkv={k.shape[1]}, S={S}, D={D}, causal, GQA), {reps} repetitions in "
-                  f"{dt:.1f} s on {threads} threads; host: {_physical_cores()} physical cores, "
+        "sample": f"libtorch CPU SDPA (SdpaOp::Compute's call on a CPU mesh) in fp32 on the bf16-rounded inputs, "
+                  f"whole workload (B={B}, Hq={Hq}, Hkv={k.shape[1]}, S={S}, D={D}, causal, GQA), {reps} "
+                  f"repetitions in {dt:.1f} s on {threads} threads; host: {_physical_cores()} physical cores, "
                   f"{os.cpu_count()} logical CPUs",
+        "bf16": {"TFLOP/s": round(rate_b / 1e12, 4), "reps": reps_b, "seconds": round(dt_b, 1),
+                 "note": "the same call on the bf16 tensors"},
     }
-    log(f"CPU baseline: {rate / 1e12:.3f} TFLOP/s on {threads} threads ({reps} reps, {dt:.1f} s)")
+    log(f"CPU baseline: fp32 {rate / 1e12:.3f} TFLOP/s ({reps} reps, {dt:.1f} s), bf16 {rate_b / 1e12:.3f} "
+        f"TFLOP/s ({reps_b} reps, {dt_b:.1f} s), {threads} threads")
     return info, out
 
 
-def secondary_workloads(torch, F, dev, timer):
+def cpu_decode_baseline(torch, qd, kc, vc, lens_np, dbytes, min_seconds):
+    """DTorch's CPU path for the decode workload: libtorch CPU SDPA per sequence over its true length
+    (is_causal=False, enable_gqa=True), fp32 on the bf16 values of the GPU run's own caches."""
+    from oracle import dtorch_cpu_path as cpu
+
+    threads = torch.get_num_threads()
+    q = qd.float().cpu()
+    ks = [kc[b:b + 1, :, :int(L)].float().cpu() for b, L in enumerate(lens_np)]
+    vs = [vc[b:b + 1, :, :int(L)].float().cpu() for b, L in enumerate(lens_np)]
+
+    def run():
+        for b in range(len(ks)):
+            cpu.sdpa(q[b:b + 1], ks[b], vs[b], enable_gqa=True)
+
+    reps, dt = _timed_reps(run, min_seconds, min_reps=2)
+    per = dt / reps
+    # the fp32 caches move twice the bf16 bytes; the rate is quoted on the workload's bf16 bytes, like the GPU's
+    info = {"GB/s": round(dbytes / per / 1e9, 2), "ms": round(per * 1e3, 2), "reps": reps, "threads": threads,
+            "sample": "64 sequences, lengths U[512, 8192], per-sequence libtorch CPU SDPA (Lq = 1, GQA 32/8) "
+                      "in fp32 on the bf16 cache values; rate on the bf16 workload bytes"}
+    log(f"CPU decode baseline: {per * 1e3:.1f} ms per batch ({dbytes / per / 1e9:.1f} GB/s of bf16 workload "
+        f"bytes), {reps} reps on {threads} threads")
+    del ks, vs
+    return info
+
+
+def secondary_workloads(torch, F, dev, timer, cpu_info=None, cpu_seconds=0.0):
     extras = {}
     flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
 
@@ -137,6 +180,8 @@ def secondary_workloads(torch, F, dev, timer):
                            "note": "L2/MALL flushed before every rep"}
     log(f"decode B=64 Hq=32 Hkv=8 lengths U[512,8192]: {med * 1e6:.1f} us, {gbs:.0f} GB/s "
         f"({100 * gbs * 1e9 / PEAK_HBM:.1f}% of HBM)")
+    if cpu_info is not None:
+        cpu_info["decode_c3"] = cpu_decode_baseline(torch, qd, kc, vc, lens_np, dbytes, cpu_seconds)
 
     # one decode step: append the new token's K/V (written at position L - 1 of each sequence, so the
     # attended length stays the bench's), then decode; lengths are reset outside the timed region
@@ -329,7 +374,7 @@ def main():
     flops = causal_flops(B, Hq, S, D)
 
     cpu_info, cpu_out = (None, None) if args.no_cpu else cpu_baseline(torch, qn, kn, vn, args.cpu_seconds)
-    extras = {} if args.no_extras else secondary_workloads(torch, F, dev, timer)
+    extras = {} if args.no_extras else secondary_workloads(torch, F, dev, timer, cpu_info, args.cpu_seconds / 2)
 
     # ---------------------------------------------------------------- headline: W warmup, K timed steps
     q, k, v = (torch.from_numpy(x).to(torch.bfloat16).to(dev) for x in (qn, kn, vn))
@@ -337,10 +382,17 @@ def main():
     def step():
         return F.scaled_dot_product_attention_with_lse(q, k, v, is_causal=True, enable_gqa=True)
 
+    # Warm-up: W steps, extended to at least HEADLINE_SETTLE_S of back-to-back launches, whatever W is,
+    # so that the timed steps never fall inside the clock ramp.
     out = None
-    for _ in range(args.warmup):
+    t_w, n_w = time.perf_counter(), 0
+    while n_w < args.warmup or time.perf_counter() - t_w < HEADLINE_SETTLE_S:
         out = step()
+        n_w += 1
+        if n_w % 16 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
+    log(f"headline warm-up: {n_w} steps in {time.perf_counter() - t_w:.3f} s")
     # One event pair on the launch stream brackets the K launches: their GPU time over K is the average
     # launch duration (it includes the dispatch gaps, so it bounds the kernel time from above).  An event
     # pair per step would add ~7 us of event packets to every step (measured: 147 -> 154 us per step).

@@ -105,7 +105,7 @@ def sdpa_fwd(
         else:
             logits = logits + m.astype(np.float64)
     logits = np.where(keep, logits, -np.inf)
-    mx = np.max(logits, axis=-1, keepdims=True)
+    mx = np.max(logits, axis=-1, keepdims=True, initial=-np.inf)  # an empty key set is fully masked
     mx_safe = np.where(np.isfinite(mx), mx, 0.0)
     p = np.exp(logits - mx_safe)
     l = np.sum(p, axis=-1, keepdims=True)

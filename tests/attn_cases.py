@@ -46,3 +46,20 @@ def lse_rel(a, b) -> float:
 
 def host(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().double().numpy()
+
+
+def cpu_path_full(q: np.ndarray, k: np.ndarray, v: np.ndarray, is_causal: bool, dtype=torch.bfloat16,
+                  prerounded: bool = False):
+    """DTorch's CPU path on every (batch, head) of a full-size case: libtorch's CPU flash attention in
+    fp32 (the kernel SdpaOp::Compute reaches on a CPU mesh, with its LSE) on the values the device
+    tensors hold (the `dtype`-rounded inputs, or `q, k, v` as given when `prerounded`).  GQA is spelled
+    out with repeat_interleave, i.e. repeat_kv.  Returns float64 (O, LSE)."""
+    from oracle import dtorch_cpu_path as cpu
+    conv = (lambda x: torch.from_numpy(np.asarray(x, dtype=np.float32))) if prerounded else (
+        lambda x: torch.from_numpy(rounded(x, dtype).astype(np.float32)))
+    tq, tk, tv = conv(q), conv(k), conv(v)
+    g = tq.shape[1] // tk.shape[1]
+    if g > 1:
+        tk, tv = tk.repeat_interleave(g, dim=1), tv.repeat_interleave(g, dim=1)
+    o, lse = cpu.sdpa_with_lse(tq, tk, tv, is_causal=is_causal)
+    return o.double().numpy(), lse.double().numpy()

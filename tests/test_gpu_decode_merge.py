@@ -162,8 +162,9 @@ def test_ring_step_small_all_ranks():
 
 def test_config4_ring_step_full_size():
     # Q chunk of 4096 tokens (global chunk 3) against 4 KV chunks of 4096: 1 causal diagonal + 3 full,
-    # Hq=32, Hkv=8, D=128, B=1, bf16; checked on sampled heads and rows against the single pass over
-    # all 16384 keys.
+    # Hq=32, Hkv=8, D=128, B=1, bf16; every head and row against DTorch's CPU path for the same step
+    # (libtorch's fp32 CPU flash attention per block, then the LSE merge), and sampled rows against the
+    # single pass over all 16384 keys (which pins the block offsets independently of the merge).
     rng = np.random.default_rng(0)
     C, Hq, Hkv, D = 4096, 32, 8, 128
     q = randn(rng, (1, Hq, C, D))
@@ -174,6 +175,14 @@ def test_config4_ring_step_full_size():
                                          return_blocks=True)
     torch.cuda.synchronize()
     assert len(blocks) == 4
+    from oracle import dtorch_cpu_path as cpu
+    f32 = lambda x: torch.from_numpy(rounded(x).astype(np.float32))
+    ro, rl = cpu.ring_step(f32(q), [f32(x) for x in k], [f32(x) for x in v], 3)
+    ho, hl = host(o), host(l)
+    err, lerr = max_abs(ho, ro), lse_rel(hl, rl)
+    print(f"C4 full size: max-abs {err:.3e}, LSE rel {lerr:.3e}")
+    assert err <= O_TOL_BF16
+    assert lerr <= LSE_TOL
     k_all = np.concatenate(k, axis=2)
     v_all = np.concatenate(v, axis=2)
     rows = np.r_[0:64, 2000:2064, 4032:4096]
@@ -181,9 +190,9 @@ def test_config4_ring_step_full_size():
         hk = h // 4
         qs = rounded(q[0, h, rows])[None]
         # global query position = 3*C + row; keys 0..16383 under the causal rule
-        ro, rl = _causal_rows(qs[0], rounded(k_all[0, hk]), rounded(v_all[0, hk]), 3 * C + rows)
-        assert max_abs(host(o[0, h, rows]), ro) <= O_TOL_BF16, h
-        assert lse_rel(host(l[0, h, rows]), rl) <= LSE_TOL, h
+        sro, srl = _causal_rows(qs[0], rounded(k_all[0, hk]), rounded(v_all[0, hk]), 3 * C + rows)
+        assert max_abs(ho[0, h, rows], sro) <= O_TOL_BF16, h
+        assert lse_rel(hl[0, h, rows], srl) <= LSE_TOL, h
 
 
 def _causal_rows(q, k, v, qpos):
@@ -350,3 +359,35 @@ def test_config3_decode_paged_full_size():
     ro, rl = orc.decode(host(tq[pick]), host(kc[pick]), host(vc[pick]), lengths[pick])
     assert max_abs(host(o[pick]), ro) <= O_TOL_BF16
     assert lse_rel(host(lse[pick]), rl[..., 0]) <= LSE_TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 4), (16, 4)])   # groups of 2 and 4 heads per kv head
+def test_decode_d64_default_splits(dtype, Hq, Hkv):
+    # D = 64 with chunk = 0 takes the 384-token default splits (96 tokens per wave): lengths on both
+    # sides of a split boundary and an empty sequence, contiguous and paged
+    lengths = np.array([383, 384, 385, 0, 1000], dtype=np.int32)
+    B, D, Smax = len(lengths), 64, 1024
+    o, lse, ro, rl = _decode_case(B, Hq, Hkv, Smax, D, lengths, chunk=0, dtype=dtype, seed=Hq + Hkv)
+    nz = lengths > 0
+    assert np.all(o[~nz] == 0) and np.all(np.isneginf(lse[~nz]))
+    assert max_abs(o[nz], ro[nz]) <= O_TOL_BF16
+    assert lse_rel(lse[nz], rl[nz]) <= LSE_TOL
+    rng = np.random.default_rng(Hq)
+    q = randn(rng, (B, Hq, 1, D))
+    kp, vp, tk, tv, bt, max_pages = _paged_pool(rng, lengths, Hkv, D, 16, dtype=dtype)
+    F = _F()
+    tq, tl = to_dev(q, dtype), torch.from_numpy(lengths).cuda()
+    po, pl = F.decode_attention_paged(tq, tk, tv, torch.from_numpy(bt).cuda(), tl, chunk=0)
+    torch.cuda.synchronize()
+    hpo, hpl = host(po), host(pl)
+    assert np.all(hpo[~nz] == 0) and np.all(np.isneginf(hpl[~nz]))
+    idx = np.flatnonzero(nz)
+    pro, prl = orc.decode_paged(rounded(q[idx], dtype), rounded(np.nan_to_num(kp), dtype),
+                                rounded(np.nan_to_num(vp), dtype), bt[idx], lengths[idx])
+    assert max_abs(hpo[idx], pro) <= O_TOL_BF16
+    assert lse_rel(hpl[idx], prl[..., 0]) <= LSE_TOL
+    S = max_pages * 16
+    co, cl = F.decode_attention(tq, _gather_dev(tk, bt, lengths, S), _gather_dev(tv, bt, lengths, S), tl, chunk=0)
+    torch.cuda.synchronize()
+    assert torch.equal(po, co) and torch.equal(pl, cl)

@@ -1,13 +1,27 @@
 """GPU parity of the fp8 e4m3fn path: the per-head quantizer bit-exact against the oracle, and the
-fp8 attention within 6e-2 of the fp32 reference on the bf16 inputs (and tighter on the dequantized
-inputs, which isolates the kernel's own error).  No reference parity exists for fp8 (DTorch's
-DataKind stops at bf16/fp16/fp32 and its quantized branch is third-party SageAttention)."""
+fp8 attention against two references:
+
+* the dequantized inputs (exact attention on code * descale): this isolates the kernel's own error
+  (P rounded to e4m3, fp32 accumulation, bf16 output) and is held to max-abs 3e-2 on O and the LSE
+  bar of 1e-3;
+* the bf16 inputs (the fp32 reference of the bf16 workload): the error also contains the input
+  quantization, whose own size is measured in the test (exact attention on the dequantized inputs
+  against the bf16 reference).  For the non-causal MMDiT workload that floor is ~2e-3 in LSE, so
+  the 1e-3 LSE bar cannot hold for per-head e4m3 inputs by construction; the test asserts O <= 6e-2
+  and LSE <= 3e-3.  For causal rows, whose few keys do not average the quantization errors away, the
+  bound is the triangle inequality: measured quantization error plus the kernel bar.
+
+No reference parity exists for fp8 (DTorch's DataKind stops at bf16/fp16/fp32 and its quantized
+branch is third-party SageAttention)."""
 import numpy as np
 import pytest
 import torch
 
 from oracle import sdpa as orc
-from tests.attn_cases import LSE_TOL, O_TOL_FP8, host, lse_rel, max_abs, randn, rounded, to_dev
+from tests.attn_cases import LSE_TOL, O_TOL_FP8, cpu_path_full, host, lse_rel, max_abs, randn, rounded, to_dev
+
+O_TOL_FP8_KERNEL = 3e-2  # max-abs against exact attention on the dequantized inputs
+LSE_TOL_FP8_INPUTS = 3e-3  # LSE against the bf16 reference: the e4m3 input floor is ~2e-3
 
 pytestmark = pytest.mark.gpu
 
@@ -51,34 +65,48 @@ def test_fp8_attention_noncausal(B, H, S, D):
     ro, rl = orc.sdpa_fwd(rounded(q), rounded(k), rounded(v))
     assert max_abs(o, ro) <= O_TOL_FP8
     # on the dequantized inputs the only error left is the kernel's own (P in e4m3, bf16 output)
-    deq = [orc.fp8_dequantize_per_head(*orc.fp8_quantize_per_head(rounded(x).astype(np.float32))) for x in (q, k, v)]
+    deq = [_deq(x) for x in (q, k, v)]
     do, dl = orc.sdpa_fwd(*deq)
-    assert max_abs(o, do) <= 3e-2
+    assert max_abs(o, do) <= O_TOL_FP8_KERNEL
     assert lse_rel(lse, dl) <= LSE_TOL
+
+
+def _deq(x):
+    return orc.fp8_dequantize_per_head(*orc.fp8_quantize_per_head(rounded(x).astype(np.float32)))
 
 
 def test_fp8_attention_causal():
-    # Per-head e4m3 quantization of Q/K/V alone moves causal rows by up to ~0.09 from the fp32
-    # reference on this case (exact attention on the dequantized inputs does), because short causal
-    # rows do not average the 3-bit-mantissa errors away.  The kernel's own error is therefore checked
-    # against the oracle on the dequantized inputs; the task's fp8 configuration (non-causal MMDiT)
-    # meets 6e-2 against the bf16 reference in test_config5b_mmdit_fp8_full_size.
+    # The kernel's own error is checked against the oracle on the dequantized inputs.  Against the bf16
+    # reference the bound is derived: |o - ref| <= |o - deq_ref| + |deq_ref - ref|, where the second
+    # term is the input quantization alone (measured here, ~0.09 on this case: short causal rows do not
+    # average the 3-bit-mantissa errors away).
     q, k, v, o, lse = _fp8_case(2, 3, 300, 128, True, seed=4)
-    deq = [orc.fp8_dequantize_per_head(*orc.fp8_quantize_per_head(rounded(x).astype(np.float32))) for x in (q, k, v)]
+    deq = [_deq(x) for x in (q, k, v)]
     do, dl = orc.sdpa_fwd(*deq, is_causal=True)
     assert max_abs(o, do) <= O_TOL_FP8  # e4m3 P (2^-4 relative) on rows with few keys
     assert lse_rel(lse, dl) <= LSE_TOL
-    ro, _ = orc.sdpa_fwd(rounded(q), rounded(k), rounded(v), is_causal=True)
-    assert max_abs(o, ro) <= 0.25
+    ro, rl = orc.sdpa_fwd(rounded(q), rounded(k), rounded(v), is_causal=True)
+    quant_floor = max_abs(do, ro)
+    print(f"causal fp8: input quantization alone moves O by {quant_floor:.3e}, LSE by {lse_rel(dl, rl):.3e}")
+    assert max_abs(o, ro) <= quant_floor + O_TOL_FP8
+    assert lse_rel(lse, rl) <= lse_rel(dl, rl) + LSE_TOL
 
 
 def test_config5b_mmdit_fp8_full_size():
-    # B=1, H=24, S=4608, D=128, non-causal, per-head absmax e4m3fn, bf16 output; sampled heads
+    # B=1, H=24, S=4608, D=128, non-causal, per-head absmax e4m3fn, bf16 output; every head and row
     q, k, v, o, lse = _fp8_case(1, 24, 4608, 128, False, seed=0)
-    for h in (0, 12, 23):
-        ro, rl = orc.sdpa_fwd(rounded(q[0, h])[None], rounded(k[0, h])[None], rounded(v[0, h])[None])
-        assert max_abs(o[0, h], ro[0]) <= O_TOL_FP8, h
-        assert lse_rel(lse[0, h], rl[0]) <= 5e-2, h
+    ro, rl = cpu_path_full(q, k, v, False)
+    deq = [_deq(x) for x in (q, k, v)]
+    do, dl = cpu_path_full(*deq, False, prerounded=True)
+    floor_o, floor_l = max_abs(do, ro), lse_rel(dl, rl)
+    e_ref, l_ref = max_abs(o, ro), lse_rel(lse, rl)
+    e_deq, l_deq = max_abs(o, do), lse_rel(lse, dl)
+    print(f"C5b full size: vs bf16 reference max-abs {e_ref:.3e} LSE {l_ref:.3e}; vs dequantized inputs "
+          f"max-abs {e_deq:.3e} LSE {l_deq:.3e}; quantization floor max-abs {floor_o:.3e} LSE {floor_l:.3e}")
+    assert e_deq <= O_TOL_FP8_KERNEL
+    assert l_deq <= LSE_TOL
+    assert e_ref <= O_TOL_FP8
+    assert l_ref <= LSE_TOL_FP8_INPUTS
 
 
 @pytest.mark.parametrize("D", [64, 128])

@@ -91,6 +91,14 @@ def test_fully_masked_rows_are_zero_with_neg_inf_lse():
     o, lse = orc.sdpa_fwd(q, k, v, is_causal=True, q_offset=0, k_offset=4)  # rows 0..3 see nothing
     assert np.all(o[..., :4, :] == 0) and np.all(np.isneginf(lse[..., :4]))
     assert np.all(np.isfinite(lse[..., 4:]))
+    # an empty key set is the same case for every row, and an empty sequence in decode likewise; the
+    # merge identity (a -inf block adds nothing) then holds for it too
+    o0, l0 = orc.sdpa_fwd(q, k[..., :0, :], v[..., :0, :])
+    assert o0.shape == q.shape and np.all(o0 == 0) and np.all(np.isneginf(l0))
+    od, ld = orc.decode(q[:, :, :1], k, v, [0])
+    assert np.all(od == 0) and np.all(np.isneginf(ld))
+    om, lm = orc.lse_merge([o0, o], [l0, lse])
+    assert np.allclose(om, o, atol=1e-15) and np.array_equal(np.isneginf(lm), np.isneginf(lse))
 
 
 # --------------------------------------------------------------------------- closed forms
