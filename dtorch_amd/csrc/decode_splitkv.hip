@@ -15,6 +15,8 @@
 // Kernel 2 (decode_merge_kernel): one wave per (b, query head) merges the ceil(L_b / C) partials by
 // LSE.  (Merging inside kernel 1 by the last workgroup needs device-scope fences; on gfx950 each one
 // writes back and invalidates the XCD's L2, which costs far more than the second launch.)
+#include <mutex>
+
 #include "dtattn_common.hpp"
 
 namespace dtattn {
@@ -392,9 +394,62 @@ extern "C" size_t dtattn_decode_workspace_size(int64_t B, int64_t Hq, int64_t S_
     return decode_ws_parts(B, Hq, S_max, D, chunk, nullptr);
 }
 
-extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_) {
-    if (a == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: args is NULL");
-    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+namespace dtattn {
+namespace {
+
+// Scratch of the allocation-free decode entry point (dtattn_decode_splitkv_noalloc): the partial
+// (O, LSE) of every split lives here instead of in a caller-provided workspace.  Each device that
+// loads the library holds its own copy until the process ends.  Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in for the symbol): the device address comes from
+// hipGetSymbolAddress, once per device with that device current, and is cached per device.
+constexpr size_t kScratchBytes = DTATTN_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+struct ScratchTable {
+    std::once_flag once[kMaxScratchDevices];
+    void* ptr[kMaxScratchDevices] = {};
+    hipError_t status[kMaxScratchDevices] = {};
+};
+ScratchTable& scratch_table() {
+    static ScratchTable t;
+    return t;
+}
+
+// Device address of `scratch` on the device `stream` belongs to (the current device for the null
+// stream).
+int scratch_address(hipStream_t stream, void** out) {
+    int dev = -1;
+    hipError_t e = stream == nullptr ? hipGetDevice(&dev) : hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+        return fail(DTATTN_ERR_DEVICE, "decode_noalloc: cannot tell the stream's device (%s)", hipGetErrorString(e));
+    ScratchTable& t = scratch_table();
+    std::call_once(t.once[dev], [&]() {
+        int cur = -1;
+        hipError_t r = hipGetDevice(&cur);
+        if (r == hipSuccess && cur != dev) r = hipSetDevice(dev);
+        void* ptr = nullptr;
+        if (r == hipSuccess) r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (cur >= 0 && cur != dev) {
+            const hipError_t back = hipSetDevice(cur);
+            if (r == hipSuccess) r = back;
+        }
+        t.status[dev] = r;
+        t.ptr[dev] = r == hipSuccess ? ptr : nullptr;
+    });
+    if (t.status[dev] != hipSuccess || t.ptr[dev] == nullptr)
+        return fail(DTATTN_ERR_DEVICE, "decode_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                    hipGetErrorString(t.status[dev]));
+    *out = t.ptr[dev];
+    return DTATTN_OK;
+}
+
+}  // namespace
+
+// The split-KV decode with its partials in `ws` (at least decode_ws_parts() bytes, 256-byte aligned),
+// or in `scratch` when `noalloc`.
+static int decode_splitkv_run(const dtattn_decode_args* a, void* ws, size_t ws_bytes, bool noalloc,
+                              hipStream_t stream) {
     if (a->B < 0 || a->Hq <= 0 || a->Hkv <= 0 || a->S_max <= 0 || a->D <= 0)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: bad sizes");
     if (a->Hq % a->Hkv != 0) return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: Hq is not a multiple of Hkv");
@@ -416,12 +471,21 @@ extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_)
         if ((s * esz) % 16 != 0) return fail(DTATTN_ERR_UNSUPPORTED, "decode: strides must be multiples of 16 bytes");
     int64_t nsplit = 0;
     const size_t need = decode_ws_parts(a->B, a->Hq, a->S_max, a->D, chunk, &nsplit);
-    if (a->workspace == nullptr || a->workspace_bytes < need)
-        return fail(DTATTN_ERR_WORKSPACE, "decode: workspace of %zu bytes required, %zu given", need,
-                    a->workspace_bytes);
-    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
-        return fail(DTATTN_ERR_WORKSPACE, "decode: workspace must be 256-byte aligned");
     if (nsplit > 65535 || a->B > 65535) return fail(DTATTN_ERR_UNSUPPORTED, "decode: grid too large");
+    if (noalloc) {
+        if (need > kScratchBytes)
+            return fail(DTATTN_ERR_WORKSPACE,
+                        "decode_noalloc: this call needs %zu bytes of scratch (B * Hq * ceil(S_max / %d) partials); "
+                        "the allocation-free entry point holds %zu",
+                        need, chunk, kScratchBytes);
+        const int st = scratch_address(stream, &ws);
+        if (st != DTATTN_OK) return st;
+        ws_bytes = kScratchBytes;
+    }
+    if (ws == nullptr || ws_bytes < need)
+        return fail(DTATTN_ERR_WORKSPACE, "decode: workspace of %zu bytes required, %zu given", need, ws_bytes);
+    if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+        return fail(DTATTN_ERR_WORKSPACE, "decode: workspace must be 256-byte aligned");
 
     DecodeParams p;
     p.q = a->q;
@@ -431,8 +495,8 @@ extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_)
     p.o = a->o;
     p.lse = a->lse;
     const size_t o_bytes = (size_t)a->B * a->Hq * nsplit * a->D * sizeof(float);
-    p.part_o = reinterpret_cast<float*>(a->workspace);
-    p.part_lse = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + ((o_bytes + 255) & ~(size_t)255));
+    p.part_o = reinterpret_cast<float*>(ws);
+    p.part_lse = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + ((o_bytes + 255) & ~(size_t)255));
     p.qs_b = a->q_stride[0], p.qs_h = a->q_stride[1];
     p.ks_b = a->k_stride[0], p.ks_h = a->k_stride[1], p.ks_s = a->k_stride[2];
     p.vs_b = a->v_stride[0], p.vs_h = a->v_stride[1], p.vs_s = a->v_stride[2];
@@ -454,6 +518,18 @@ extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_)
     if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, false>(p, (int)a->D, stream);
     if (a->dtype == DTATTN_FP32) return dispatch_decode<float, false>(p, (int)a->D, stream);
     return dispatch_decode<f16_t, false>(p, (int)a->D, stream);
+}
+
+}  // namespace dtattn
+
+extern "C" int dtattn_decode_splitkv(const dtattn_decode_args* a, void* stream_) {
+    if (a == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode: args is NULL");
+    return decode_splitkv_run(a, a->workspace, a->workspace_bytes, false, reinterpret_cast<hipStream_t>(stream_));
+}
+
+extern "C" int dtattn_decode_splitkv_noalloc(const dtattn_decode_args* a, void* stream_) {
+    if (a == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "decode_noalloc: args is NULL");
+    return decode_splitkv_run(a, nullptr, 0, true, reinterpret_cast<hipStream_t>(stream_));
 }
 
 extern "C" size_t dtattn_decode_paged_workspace_size(int64_t B, int64_t Hq, int64_t max_pages, int64_t page_size,

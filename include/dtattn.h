@@ -120,6 +120,22 @@ typedef struct {
 size_t dtattn_decode_workspace_size(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk);
 int dtattn_decode_splitkv(const dtattn_decode_args* args, void* stream);
 
+/* Allocation-free variant of dtattn_decode_splitkv.
+ *
+ * No counterpart in the reference.  For callers that cannot allocate device memory at call time: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.  Same arguments,
+ * kernels and results (bit-identical) as dtattn_decode_splitkv, except that `workspace` and
+ * `workspace_bytes` are ignored: the split partials live in a device array of
+ * DTATTN_NOALLOC_SCRATCH_BYTES that the library holds on each device it runs on until the process
+ * ends (its address is looked up once per device, on the first call there).  A call whose partials
+ * need more than that (dtattn_decode_workspace_size() with the call's chunk) returns
+ * DTATTN_ERR_WORKSPACE.  Nothing is allocated and nothing needs clearing between calls; every call on
+ * one device shares the array, so calls that overlap in time on one device (two streams, or two host
+ * threads) race and must be ordered by the caller.
+ */
+#define DTATTN_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int dtattn_decode_splitkv_noalloc(const dtattn_decode_args* args, void* stream);
+
 /* Split-KV single-token decode against a paged KV cache.
  *
  * No counterpart in the reference (the next step its survey lists for decode: a KV cache feeding the
