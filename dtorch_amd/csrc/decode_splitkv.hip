@@ -43,6 +43,8 @@ struct DecodeParams {
     const int32_t* block_table;
     int64_t bt_s;
     int32_t page_shift, num_pages;
+    // real head dim (<= the kernel's D; a multiple of 16 bytes of elements) and its 16-byte chunks
+    int32_t d_real, d_ch;
 };
 
 constexpr int kDecodeChunk = 128;  // smallest split; workspace queries with chunk 0 size for it
@@ -58,7 +60,13 @@ static int32_t auto_chunk(int64_t Hq, int64_t Hkv, int64_t esz) {
     return esz == 2 ? 384 : 256;
 }
 
-size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D, int32_t chunk, int64_t* nsplit_out) {
+// Kernel head dim for a real head dim: 64 or 128 (0: unsupported).  Smaller real dims run the
+// kernel of the next size, reading a valid chunk in place of each padded one with its query chunk
+// zeroed, so the padding adds nothing to the scores; the padded output columns are not stored.
+static int decode_kernel_dim(int64_t D) { return D <= 0 ? 0 : D <= 64 ? 64 : D <= 128 ? 128 : 0; }
+
+size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D_real, int32_t chunk, int64_t* nsplit_out) {
+    const int64_t D = decode_kernel_dim(D_real) > 0 ? decode_kernel_dim(D_real) : D_real;  // partials are kernel-wide
     const int64_t nsplit = (S_max + chunk - 1) / chunk;
     if (nsplit_out) *nsplit_out = nsplit;
     const size_t o_bytes = (size_t)B * Hq * nsplit * D * sizeof(float);
@@ -103,20 +111,24 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     if (L == 0) {  // empty sequence: O = 0, LSE = -inf
         if (split == 0)
             for (int idx = tid; idx < G * D; idx += 256) {
-                obase[(hq0 + idx / D) * p.os_h + idx % D] = Elem<T>::from_f32(0.f);
+                if (idx % D < p.d_real) obase[(hq0 + idx / D) * p.os_h + idx % D] = Elem<T>::from_f32(0.f);
                 if (p.lse != nullptr && idx % D == 0) p.lse[b * p.lses_b + hq0 + idx / D] = kNegInf;
             }
         return;
     }
     if (t0 >= L) return;
     const int n_tok = min(C, L - t0);
-    const int c8 = lane % LPT;           // 16-byte chunk of the row this lane reads
+    const int c8r = lane % LPT;          // 16-byte chunk of the row this lane covers
+    const bool cvalid = c8r < p.d_ch;    // false only for a padded head dim
+    const int c8 = cvalid ? c8r : 0;     // the chunk it reads: a valid one (its query chunk is zero)
     const int tsub = lane / LPT;
 
     u32x4 qv[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g) {
         qv[g] = ld16(reinterpret_cast<const T*>(p.q) + b * p.qs_b + (hq0 + g) * p.qs_h + c8 * EPC);
+        if (!cvalid) qv[g] = u32x4{0u, 0u, 0u, 0u};
+    }
 
     const int kpitch = (int)(p.ks_s * (int64_t)sizeof(T));
     const int vpitch = (int)(p.vs_s * (int64_t)sizeof(T));
@@ -124,8 +136,9 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     const int64_t vbo = PAGED ? 0 : b * p.vs_b + (int64_t)t0 * p.vs_s;
     const T* kp = reinterpret_cast<const T*>(p.k) + hk * p.ks_h + kbo;
     const T* vp = reinterpret_cast<const T*>(p.v) + hk * p.vs_h + vbo;
-    const auto krs = make_rsrc(kp, (uint32_t)((n_tok - 1) * kpitch + D * (int)sizeof(T)));
-    const auto vrs = make_rsrc(vp, (uint32_t)((n_tok - 1) * vpitch + D * (int)sizeof(T)));
+    // the resources end where the chunk's last valid row ends (at the real head dim)
+    const auto krs = make_rsrc(kp, (uint32_t)((n_tok - 1) * kpitch + p.d_real * (int)sizeof(T)));
+    const auto vrs = make_rsrc(vp, (uint32_t)((n_tok - 1) * vpitch + p.d_real * (int)sizeof(T)));
     const int32_t* bt = PAGED ? p.block_table + b * p.bt_s : nullptr;
 
     float m[G], l[G], acc[G][EPC];
@@ -281,7 +294,7 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
         }
         const int hq = hq0 + g;
         if (single) {  // the whole sequence was this chunk: final output
-            obase[hq * p.os_h + d] = Elem<T>::from_f32(val / Lsum);
+            if (d < p.d_real) obase[hq * p.os_h + d] = Elem<T>::from_f32(val / Lsum);
             if (p.lse != nullptr && d == 0) p.lse[b * p.lses_b + hq] = (M + __log2f(Lsum)) * kLn2;
         } else {
             p.part_o[(((int64_t)b * p.Hq + hq) * p.nsplit + split) * D + d] = val / Lsum;
@@ -335,7 +348,8 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p)
     }
     T* op = reinterpret_cast<T*>(p.o) + b * p.os_b + hq * p.os_h;
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) op[lane * DPL + e] = Elem<T>::from_f32(acc[e]);
+    for (int e = 0; e < DPL; ++e)
+        if (lane * DPL + e < p.d_real) op[lane * DPL + e] = Elem<T>::from_f32(acc[e]);
     if (p.lse != nullptr && lane == 0) p.lse[b * p.lses_b + hq] = mx + __logf(sum);
 }
 
@@ -377,11 +391,17 @@ static int dispatch_group(const DecodeParams& p, hipStream_t stream) {
     return dispatch_chunk<T, D, 1, PAGED>(p, stream);
 }
 
+// D: the real head dim (a multiple of 16 bytes of elements, up to 128).
 template <typename T, bool PAGED>
-static int dispatch_decode(const DecodeParams& p, int D, hipStream_t stream) {
-    if (D == 128) return dispatch_group<T, 128, PAGED>(p, stream);
-    if (D == 64) return dispatch_group<T, 64, PAGED>(p, stream);
-    return fail(DTATTN_ERR_UNSUPPORTED, "decode: head dim %d not supported (64 or 128)", D);
+static int dispatch_decode(DecodeParams p, int D, hipStream_t stream) {
+    const int Dk = decode_kernel_dim(D);
+    if (Dk == 0 || (D * (int)sizeof(T)) % 16 != 0)
+        return fail(DTATTN_ERR_UNSUPPORTED, "decode: head dim %d not supported (a multiple of %d up to 128)", D,
+                    16 / (int)sizeof(T));
+    p.d_real = D;
+    p.d_ch = D * (int)sizeof(T) / 16;
+    if (Dk == 128) return dispatch_group<T, 128, PAGED>(p, stream);
+    return dispatch_group<T, 64, PAGED>(p, stream);
 }
 
 }  // namespace dtattn
@@ -494,7 +514,7 @@ static int decode_splitkv_run(const dtattn_decode_args* a, void* ws, size_t ws_b
     p.lengths = a->lengths;
     p.o = a->o;
     p.lse = a->lse;
-    const size_t o_bytes = (size_t)a->B * a->Hq * nsplit * a->D * sizeof(float);
+    const size_t o_bytes = (size_t)a->B * a->Hq * nsplit * (decode_kernel_dim(a->D) > 0 ? decode_kernel_dim(a->D) : a->D) * sizeof(float);
     p.part_o = reinterpret_cast<float*>(ws);
     p.part_lse = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + ((o_bytes + 255) & ~(size_t)255));
     p.qs_b = a->q_stride[0], p.qs_h = a->q_stride[1];
@@ -582,7 +602,7 @@ extern "C" int dtattn_decode_paged(const dtattn_decode_paged_args* a, void* stre
     p.lengths = a->lengths;
     p.o = a->o;
     p.lse = a->lse;
-    const size_t o_bytes = (size_t)a->B * a->Hq * nsplit * a->D * sizeof(float);
+    const size_t o_bytes = (size_t)a->B * a->Hq * nsplit * (decode_kernel_dim(a->D) > 0 ? decode_kernel_dim(a->D) : a->D) * sizeof(float);
     p.part_o = reinterpret_cast<float*>(a->workspace);
     p.part_lse = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + ((o_bytes + 255) & ~(size_t)255));
     p.qs_b = a->q_stride[0], p.qs_h = a->q_stride[1];

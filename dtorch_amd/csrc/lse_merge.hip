@@ -23,6 +23,7 @@ struct MergeParams {
     int64_t slabs;  // B * H
     int32_t H, S, n;
     int32_t wg_per_slab;  // ceil(S * D / 8 / 256)
+    int32_t cpr;          // 16-byte chunks per row (D / 8); read by the generic (D = 0) instantiation
 };
 
 // Block outputs are read exactly once: non-temporal loads (load_chunk<TI, true>).  The merged output
@@ -45,12 +46,13 @@ __device__ __forceinline__ void store8<float>(float* p, const float* in) {
     __builtin_nontemporal_store(f32x4{in[4], in[5], in[6], in[7]}, reinterpret_cast<f32x4*>(p + 4));
 }
 
+// D = 0: any head dim that is a multiple of 8, with the row split computed at run time.
 template <typename TI, typename TO, int D, int NB>
 __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeParams p) {
-    constexpr int CPR = D / 8;  // chunks per row (a power of two)
     const int64_t bh = blockIdx.x / p.wg_per_slab;  // wave-uniform
     const int idx = (int)(blockIdx.x - bh * p.wg_per_slab) * 256 + (int)threadIdx.x;
-    const int s = idx / CPR, c = idx % CPR;
+    const int cpr = D > 0 ? D / 8 : p.cpr;  // chunks per row (a power of two when D > 0)
+    const int s = idx / cpr, c = idx - s * cpr;
     if (s >= p.S) return;
     const int h = (int)(bh % p.H);
     const int64_t b = bh / p.H;
@@ -121,7 +123,7 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeParams p) {
 template <typename TI, typename TO, int D>
 static int launch_merge(const MergeParams& p, hipStream_t stream) {
     MergeParams q = p;
-    q.wg_per_slab = (int32_t)(((int64_t)p.S * (D / 8) + 255) / 256);
+    q.wg_per_slab = (int32_t)(((int64_t)p.S * p.cpr + 255) / 256);
     const int64_t blocks = p.slabs * q.wg_per_slab;
     if (blocks == 0) return DTATTN_OK;
     if (blocks > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "merge: grid too large");
@@ -143,7 +145,9 @@ template <typename TI, typename TO>
 static int dispatch_merge_d(const MergeParams& p, int D, hipStream_t stream) {
     if (D == 128) return launch_merge<TI, TO, 128>(p, stream);
     if (D == 64) return launch_merge<TI, TO, 64>(p, stream);
-    return fail(DTATTN_ERR_UNSUPPORTED, "merge: head dim %d not supported (64 or 128)", D);
+    if (D == 256) return launch_merge<TI, TO, 256>(p, stream);
+    if (D == 512) return launch_merge<TI, TO, 512>(p, stream);
+    return launch_merge<TI, TO, 0>(p, stream);
 }
 
 template <typename TI>
@@ -165,8 +169,12 @@ extern "C" int dtattn_lse_merge(const dtattn_merge_args* a, void* stream_) {
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: n_blocks=%d outside [1, %d]", a->n_blocks,
                     DTATTN_MAX_MERGE_BLOCKS);
     if (a->B < 0 || a->H < 0 || a->S < 0 || a->D <= 0) return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: bad sizes");
+    if (a->D % 8 != 0 || a->D > 4096)
+        return fail(DTATTN_ERR_UNSUPPORTED, "merge: head dim %lld must be a multiple of 8 up to 4096", (long long)a->D);
     if (a->B == 0 || a->H == 0 || a->S == 0) return DTATTN_OK;
-    if (a->S > (1 << 26) || a->H > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "merge: sizes too large");
+    // chunk indices within one (batch, head) slab are int32
+    if (a->S * (a->D / 8) >= ((int64_t)1 << 31) || a->H > 0x7fffffff)
+        return fail(DTATTN_ERR_UNSUPPORTED, "merge: sizes too large");
     if (a->o == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: null output");
     const int in_esz = a->block_dtype == DTATTN_FP32 ? 4 : 2;
     const int out_esz = a->o_dtype == DTATTN_FP32 ? 4 : 2;
@@ -195,6 +203,7 @@ extern "C" int dtattn_lse_merge(const dtattn_merge_args* a, void* stream_) {
     p.H = (int32_t)a->H;
     p.S = (int32_t)a->S;
     p.n = a->n_blocks;
+    p.cpr = (int32_t)(a->D / 8);
     const int D = (int)a->D;
     if (a->block_dtype == DTATTN_BF16) return dispatch_merge_o<bf16_t>(p, D, a->o_dtype, stream);
     if (a->block_dtype == DTATTN_FP16) return dispatch_merge_o<f16_t>(p, D, a->o_dtype, stream);

@@ -41,7 +41,9 @@ __device__ __forceinline__ int kswz(int r) {
     return D >= 128 ? 4 * (r & 3) + ((r >> 2) & 3) : 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
 }
 
-template <typename T, int D, int QT, bool CAUSAL, bool MASKED>
+// PAD: the real head dims are below D (any multiple of 8, Dv may differ from D); Q/K chunks past
+// p.qk_ch and V chunks past p.v_ch load as zeros, and O chunks past p.v_ch are not stored.
+template <typename T, int D, int QT, bool CAUSAL, bool MASKED, bool PAD>
 __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams p) {
     constexpr int NW = 4;
     constexpr int BN = 64;
@@ -95,7 +97,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             u32x4 raw = {0u, 0u, 0u, 0u};
-            if (qrow < p.Sq) raw = ld16(qp + (int64_t)qrow * p.qs_s + ks * 16 + hf * 8);
+            if (qrow < p.Sq && (!PAD || 2 * ks + hf < p.qk_ch)) raw = ld16(qp + (int64_t)qrow * p.qs_s + ks * 16 + hf * 8);
             qf[ks] = __builtin_bit_cast(V8, raw);
         }
     }
@@ -113,19 +115,21 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     // Tile t of K or V -> LDS by direct buffer->LDS loads: one wave instruction fills 1 KB of LDS (lane
     // l -> byte 16*l), i.e. 1024/(2*D) rows, so lane l loads the global chunk that belongs at its LDS
     // slot, c = slot ^ kswz(row).  The buffer resource covers the tile's valid rows; rows past Sk
-    // read zeros.
-    auto dma = [&](T* dst, const T* base, int pitch, int64_t stride, int t) {
+    // read zeros, and so do chunks at or past valid_ch (PAD), whose offset is the resource's size.
+    auto dma = [&](T* dst, const T* base, int pitch, int64_t stride, int t, int valid_ch) {
         constexpr int ROWS_PER_INSTR = 1024 / (2 * D);
         constexpr int INSTR = BN / ROWS_PER_INSTR / NW;  // per wave
         const int rows = min(BN, p.Sk - t * BN);
-        const auto rs = make_rsrc(base + (int64_t)t * BN * stride,
-                                  (uint32_t)((rows - 1) * pitch + D * (int)sizeof(T)));
+        // the resource ends where the tile's last valid row ends (its real width under PAD)
+        const uint32_t nbytes = (uint32_t)((rows - 1) * pitch + (PAD ? valid_ch * 16 : D * (int)sizeof(T)));
+        const auto rs = make_rsrc(base + (int64_t)t * BN * stride, nbytes);
 #pragma unroll
         for (int i = 0; i < INSTR; ++i) {
             const int r0 = (wave * INSTR + i) * ROWS_PER_INSTR;
             const int r = r0 + lane / DCH;
             const int c = (lane % DCH) ^ kswz<D>(r);
-            buf_ld16_lds_async(rs, dst + r0 * D, (uint32_t)(r * pitch + c * 16));
+            const uint32_t off = (PAD && c >= valid_ch) ? nbytes : (uint32_t)(r * pitch + c * 16);
+            buf_ld16_lds_async(rs, dst + r0 * D, off);
         }
     };
 
@@ -150,8 +154,8 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
         lds_barrier();  // tile t landed everywhere; every wave finished tile t-1 (so Kn/Vn are free)
         auto next_tile = [&]() {
             if (t + 1 < nt) {
-                dma(Kn, kp, krow, p.ks_s, t + 1);
-                dma(Vn, vp, vrow, p.vs_s, t + 1);
+                dma(Kn, kp, krow, p.ks_s, t + 1, p.qk_ch);
+                dma(Vn, vp, vrow, p.vs_s, t + 1, p.v_ch);
             }
         };
         // Issue point of the next tile's loads: at the tile start in the causal kernel; after this tile's
@@ -294,8 +298,8 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     };
 
     if (nt > 0) {
-        dma(Ka, kp, krow, p.ks_s, 0);
-        dma(Va, vp, vrow, p.vs_s, 0);
+        dma(Ka, kp, krow, p.ks_s, 0, p.qk_ch);
+        dma(Va, vp, vrow, p.vs_s, 0, p.v_ch);
     }
     // Q fragments (and tile 0) complete here, visibly to the compiler, so that it inserts no load
     // waits inside the loop (where they would also drain the asynchronous tile loads).
@@ -338,13 +342,13 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
         const int id = it * 64 + lane;
         const int row = id / DCH, c = id % DCH;
         const int qrow = wq0 + row;
-        if (qrow < p.Sq) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Os + row * D + 8 * (c ^ (row % DCH))));
+        if (qrow < p.Sq && (!PAD || c < p.v_ch)) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Os + row * D + 8 * (c ^ (row % DCH))));
     }
 }
 
 // ------------------------------------------------------------------------------------------------
 
-template <typename T, int D, int QT, bool CAUSAL, bool MASKED>
+template <typename T, int D, int QT, bool CAUSAL, bool MASKED, bool PAD>
 static int launch_prefill(const PrefillParams& prm, hipStream_t stream) {
     constexpr int BM = 4 * QT * 32;
     PrefillParams p = prm;
@@ -352,32 +356,36 @@ static int launch_prefill(const PrefillParams& prm, hipStream_t stream) {
     const int64_t grid = (int64_t)p.n_qblocks * p.B * p.Hq;
     if (grid == 0) return DTATTN_OK;
     if (grid > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill grid too large (%lld blocks)", (long long)grid);
-    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, QT, CAUSAL, MASKED>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, QT, CAUSAL, MASKED, PAD>), dim3((unsigned)grid), dim3(256), 0, stream, p);
     return check_launch("prefill_fwd_kernel");
 }
 
-template <typename T, bool MASKED>
+template <typename T, bool MASKED, bool PAD>
 static int dispatch_prefill_m(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
     if (D == 128) {
-        return causal ? launch_prefill<T, 128, 1, true, MASKED>(p, stream)
-                      : launch_prefill<T, 128, 1, false, MASKED>(p, stream);
+        return causal ? launch_prefill<T, 128, 1, true, MASKED, PAD>(p, stream)
+                      : launch_prefill<T, 128, 1, false, MASKED, PAD>(p, stream);
     }
     if (D == 64) {
-        return causal ? launch_prefill<T, 64, 1, true, MASKED>(p, stream)
-                      : launch_prefill<T, 64, 1, false, MASKED>(p, stream);
+        return causal ? launch_prefill<T, 64, 1, true, MASKED, PAD>(p, stream)
+                      : launch_prefill<T, 64, 1, false, MASKED, PAD>(p, stream);
     }
-    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %d not supported (64, 128, 256 or 512)", D);
+    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: kernel head dim %d not supported (64, 128, 256 or 512)", D);
 }
 
+// D is the kernel's head dim (64 or 128); pad: the real head dims are below it.
 template <typename T>
-static int dispatch_prefill(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
-    return p.mask != nullptr ? dispatch_prefill_m<T, true>(p, D, causal, stream)
-                             : dispatch_prefill_m<T, false>(p, D, causal, stream);
+static int dispatch_prefill(const PrefillParams& p, int D, bool causal, bool pad, hipStream_t stream) {
+    if (pad)
+        return p.mask != nullptr ? dispatch_prefill_m<T, true, true>(p, D, causal, stream)
+                                 : dispatch_prefill_m<T, false, true>(p, D, causal, stream);
+    return p.mask != nullptr ? dispatch_prefill_m<T, true, false>(p, D, causal, stream)
+                             : dispatch_prefill_m<T, false, false>(p, D, causal, stream);
 }
 
 int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_t stream);
 int prefill_f32(const PrefillParams& p, int D, bool causal, hipStream_t stream);
-int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, hipStream_t stream);
+int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, bool pad, hipStream_t stream);
 
 static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
@@ -394,9 +402,16 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     if (a->Hq % a->Hkv != 0)
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill: Hq=%lld is not a multiple of Hkv=%lld", (long long)a->Hq,
                     (long long)a->Hkv);
-    if (a->D != a->Dv)
-        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: D=%lld != Dv=%lld not supported", (long long)a->D,
+    if (a->D <= 0 || a->Dv <= 0)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill: bad head dims D=%lld Dv=%lld", (long long)a->D,
                     (long long)a->Dv);
+    const bool sixteen_bit = a->dtype == DTATTN_BF16 || a->dtype == DTATTN_FP16;
+    if (a->D != a->Dv && !sixteen_bit)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: D=%lld != Dv=%lld is supported for bf16/fp16 only",
+                    (long long)a->D, (long long)a->Dv);
+    if (sixteen_bit && (a->D % 8 != 0 || a->Dv % 8 != 0))
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dims must be multiples of 8 (D=%lld, Dv=%lld)",
+                    (long long)a->D, (long long)a->Dv);
     // Sequence lengths up to 2^29 keep every causal index expression of the kernels in int32.
     if (a->Sq > (1 << 29) || a->Sk > (1 << 29) || a->B * a->Hq > 0x3fffffff)
         return fail(DTATTN_ERR_UNSUPPORTED, "prefill: sequence length exceeds 2^29");
@@ -476,10 +491,21 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     p.mask = a->mask;
     p.ms_b = a->mask_stride[0], p.ms_h = a->mask_stride[1], p.ms_l = a->mask_stride[2];
     p.inv_scale = 1.0f / scale;
-    const int D = (int)a->D;
     const bool causal = a->causal != 0;
-    if (a->dtype == DTATTN_FP32) return prefill_f32(p, D, causal, stream);
-    if (D == 256 || D == 512) return prefill_wide(p, D, causal, a->dtype == DTATTN_BF16, stream);
-    if (a->dtype == DTATTN_BF16) return dispatch_prefill<bf16_t>(p, D, causal, stream);
-    return dispatch_prefill<f16_t>(p, D, causal, stream);
+    if (a->dtype == DTATTN_FP32) {
+        p.qk_ch = p.v_ch = (int32_t)(a->D / 4);
+        return prefill_f32(p, (int)a->D, causal, stream);
+    }
+    // bf16 / fp16: the kernel head dim is the smallest of 64, 128, 256, 512 that holds both real head
+    // dims; smaller real dims (multiples of 8, D and Dv independent) run the padded instantiations.
+    const int64_t dmax = a->D > a->Dv ? a->D : a->Dv;
+    const int Dk = dmax <= 64 ? 64 : dmax <= 128 ? 128 : dmax <= 256 ? 256 : dmax <= 512 ? 512 : 0;
+    if (Dk == 0)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %lld exceeds 512", (long long)dmax);
+    p.qk_ch = (int32_t)(a->D / 8);
+    p.v_ch = (int32_t)(a->Dv / 8);
+    const bool pad = a->D != Dk || a->Dv != Dk;
+    if (Dk >= 256) return prefill_wide(p, Dk, causal, a->dtype == DTATTN_BF16, pad, stream);
+    if (a->dtype == DTATTN_BF16) return dispatch_prefill<bf16_t>(p, Dk, causal, pad, stream);
+    return dispatch_prefill<f16_t>(p, Dk, causal, pad, stream);
 }

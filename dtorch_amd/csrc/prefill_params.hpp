@@ -29,6 +29,10 @@ struct PrefillParams {
     const float* mask;
     int64_t ms_b, ms_h, ms_l;
     float inv_scale;
+    // Head dims below the kernel's D (PAD kernels): Q/K rows hold qk_ch valid 16-byte chunks and V/O rows
+    // v_ch; the chunks past them load as zeros (adding nothing to the scores, giving O columns that are
+    // never stored).
+    int32_t qk_ch, v_ch;
 };
 
 // Lazy rescaling: the running max only moves (and O, l are only rescaled) when some row's max grew

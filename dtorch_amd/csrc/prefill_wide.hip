@@ -25,7 +25,9 @@ namespace dtattn {
 // takes 4 aligned chunks of 4 rows); rows are whole multiples of 256 bytes, so every row starts on bank 0.
 __device__ __forceinline__ int wswz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
 
-template <typename T, int D, bool CAUSAL, bool MASKED>
+// PAD: real head dims below D (multiples of 8, Dv may differ from D), as in the main kernel: Q/K chunks
+// past p.qk_ch and V chunks past p.v_ch load as zeros, O chunks past p.v_ch are not stored.
+template <typename T, int D, bool CAUSAL, bool MASKED, bool PAD>
 __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParams p) {
     constexpr int NW = 4;
     constexpr int BN = 32;           // keys per tile
@@ -75,7 +77,8 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             u32x4 raw = {0u, 0u, 0u, 0u};
-            if (qrow < p.Sq) raw = ld16(qp + (int64_t)qrow * p.qs_s + d0 + ks * 16 + hf * 8);
+            if (qrow < p.Sq && (!PAD || (d0 >> 3) + 2 * ks + hf < p.qk_ch))
+                raw = ld16(qp + (int64_t)qrow * p.qs_s + d0 + ks * 16 + hf * 8);
             qf[ks] = __builtin_bit_cast(V8, raw);
         }
     }
@@ -90,18 +93,21 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
     const int vrow = (int)(p.vs_s * (int64_t)sizeof(T));
 
     // Tile t -> LDS (lane l -> byte 16*l of a 1 KB block, 1024 / (2 D) rows per instruction), chunk c of
-    // row r at c ^ wswz(r); rows past Sk read zeros.
-    auto dma = [&](T* dst, const T* base, int pitch, int64_t stride, int t) {
+    // row r at c ^ wswz(r); rows past Sk read zeros, and so do chunks at or past valid_ch (PAD).
+    auto dma = [&](T* dst, const T* base, int pitch, int64_t stride, int t, int valid_ch) {
         constexpr int ROWS_PER_INSTR = 1024 / (2 * D);
         constexpr int INSTR = BN / ROWS_PER_INSTR / NW;
         const int rows = min(BN, p.Sk - t * BN);
-        const auto rs = make_rsrc(base + (int64_t)t * BN * stride, (uint32_t)((rows - 1) * pitch + D * (int)sizeof(T)));
+        // the resource ends where the tile's last valid row ends (its real width under PAD)
+        const uint32_t nbytes = (uint32_t)((rows - 1) * pitch + (PAD ? valid_ch * 16 : D * (int)sizeof(T)));
+        const auto rs = make_rsrc(base + (int64_t)t * BN * stride, nbytes);
 #pragma unroll
         for (int i = 0; i < INSTR; ++i) {
             const int r0 = (wave * INSTR + i) * ROWS_PER_INSTR;
             const int r = r0 + lane / DCH;
             const int c = (lane % DCH) ^ wswz(r);
-            buf_ld16_lds_async(rs, dst + r0 * D, (uint32_t)(r * pitch + c * 16));
+            const uint32_t off = (PAD && c >= valid_ch) ? nbytes : (uint32_t)(r * pitch + c * 16);
+            buf_ld16_lds_async(rs, dst + r0 * D, off);
         }
     };
 
@@ -122,8 +128,8 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
         wait_vmem();
         lds_barrier();  // tile t landed; every wave finished tile t-1, including its exchange reads
         if (t + 1 < nt) {
-            dma(Kn, kp, krow, p.ks_s, t + 1);
-            dma(Vn, vp, vrow, p.vs_s, t + 1);
+            dma(Kn, kp, krow, p.ks_s, t + 1, p.qk_ch);
+            dma(Vn, vp, vrow, p.vs_s, t + 1, p.v_ch);
         }
         const int kbase = t * BN;
         const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && (kbase + BN - 1 > q0 + p.delta));
@@ -225,8 +231,8 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
     };
 
     if (nt > 0) {
-        dma(Ka, kp, krow, p.ks_s, 0);
-        dma(Va, vp, vrow, p.vs_s, 0);
+        dma(Ka, kp, krow, p.ks_s, 0, p.qk_ch);
+        dma(Va, vp, vrow, p.vs_s, 0, p.v_ch);
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): Q and tile 0, visibly to the compiler
     for (int t = 0; t < nt; t += 2) {
@@ -263,37 +269,44 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
         const int id = it * 256 + tid;
         const int row = id / DCH, c = id % DCH;
         const int qrow = q0 + row;
-        if (qrow < p.Sq) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Ka + row * D + 8 * (c ^ (row & 15))));
+        if (qrow < p.Sq && (!PAD || c < p.v_ch)) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Ka + row * D + 8 * (c ^ (row & 15))));
     }
 }
 
-template <typename T, int D, bool CAUSAL, bool MASKED>
+template <typename T, int D, bool CAUSAL, bool MASKED, bool PAD>
 static int launch_wide(const PrefillParams& prm, hipStream_t stream) {
     PrefillParams p = prm;
     p.n_qblocks = (p.Sq + 31) / 32;
     const int64_t grid = (int64_t)p.n_qblocks * p.B * p.Hq;
     if (grid == 0) return DTATTN_OK;
     if (grid > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill grid too large (%lld blocks)", (long long)grid);
-    hipLaunchKernelGGL((prefill_wide_kernel<T, D, CAUSAL, MASKED>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((prefill_wide_kernel<T, D, CAUSAL, MASKED, PAD>), dim3((unsigned)grid), dim3(256), 0, stream, p);
     return check_launch("prefill_wide_kernel");
 }
 
-template <typename T, bool MASKED>
+template <typename T, bool MASKED, bool PAD>
 static int dispatch_wide_m(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
     if (D == 256)
-        return causal ? launch_wide<T, 256, true, MASKED>(p, stream) : launch_wide<T, 256, false, MASKED>(p, stream);
+        return causal ? launch_wide<T, 256, true, MASKED, PAD>(p, stream)
+                      : launch_wide<T, 256, false, MASKED, PAD>(p, stream);
     if (D == 512)
-        return causal ? launch_wide<T, 512, true, MASKED>(p, stream) : launch_wide<T, 512, false, MASKED>(p, stream);
-    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %d not supported (64, 128, 256 or 512)", D);
+        return causal ? launch_wide<T, 512, true, MASKED, PAD>(p, stream)
+                      : launch_wide<T, 512, false, MASKED, PAD>(p, stream);
+    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: kernel head dim %d not supported (64, 128, 256 or 512)", D);
 }
 
-// Entry from dtattn_prefill_fwd for D = 256 / 512 with bf16 or fp16 inputs.
-int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, hipStream_t stream) {
-    if (bf16)
-        return p.mask != nullptr ? dispatch_wide_m<bf16_t, true>(p, D, causal, stream)
-                                 : dispatch_wide_m<bf16_t, false>(p, D, causal, stream);
-    return p.mask != nullptr ? dispatch_wide_m<f16_t, true>(p, D, causal, stream)
-                             : dispatch_wide_m<f16_t, false>(p, D, causal, stream);
+template <typename T>
+static int dispatch_wide(const PrefillParams& p, int D, bool causal, bool pad, hipStream_t stream) {
+    if (pad)
+        return p.mask != nullptr ? dispatch_wide_m<T, true, true>(p, D, causal, stream)
+                                 : dispatch_wide_m<T, false, true>(p, D, causal, stream);
+    return p.mask != nullptr ? dispatch_wide_m<T, true, false>(p, D, causal, stream)
+                             : dispatch_wide_m<T, false, false>(p, D, causal, stream);
+}
+
+// Entry from dtattn_prefill_fwd for kernel head dims 256 / 512 with bf16 or fp16 inputs.
+int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, bool pad, hipStream_t stream) {
+    return bf16 ? dispatch_wide<bf16_t>(p, D, causal, pad, stream) : dispatch_wide<f16_t>(p, D, causal, pad, stream);
 }
 
 }  // namespace dtattn

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define DTATTN_ABI_VERSION 5
+#define DTATTN_ABI_VERSION 6
 
 typedef enum {
     DTATTN_OK = 0,
@@ -53,7 +53,10 @@ typedef enum {
  * dtype: BF16 or FP16 (inputs and output, fp32 softmax and accumulation); FP32 (inputs and output,
  * every step in fp32: the fp32 matrix cores, no 16-bit rounding of P; ABI version 5); or FP8_E4M3FN
  * inputs with descales and a BF16 output.
- * Head dims: D == Dv; D in {64, 128}, and for BF16/FP16 also {256, 512} (ABI version 5).
+ * Head dims: BF16/FP16 take any D and Dv that are multiples of 8 up to 512, independently (the output
+ * takes v's last axis, as scaled_dot_product_attention_op.cc:26-29 does); the kernels run at 64, 128,
+ * 256 or 512 and read the columns past the real dims as zeros (ABI version 6).  FP32 and FP8 take
+ * D == Dv in {64, 128}.
  */
 typedef struct {
     const void* q; /* [B, Hq, Sq, D] */
@@ -93,7 +96,8 @@ int dtattn_prefill_fwd(const dtattn_prefill_args* args, void* stream);
  * defined as SdpaOp::Compute's arithmetic (scaled_dot_product_attention_op.cc:107-109) with Lq = 1,
  * is_causal = False and GQA, over keys [0, lengths[b]).  Cache rows at or past lengths[b] are never
  * read.  Each (b, kv head, chunk of `chunk` tokens) is one work item writing a partial (O, LSE)
- * into the workspace; a second kernel merges the partials by LSE.
+ * into the workspace; a second kernel merges the partials by LSE.  Head dims: any multiple of 16 bytes
+ * of elements up to 128 (8 for BF16/FP16, 4 for FP32; ABI version 6; the kernels run at 64 or 128).
  */
 typedef struct {
     const void* q;         /* [B, Hq, 1, D] */
@@ -226,7 +230,7 @@ int dtattn_kv_append_paged(const dtattn_kv_append_paged_args* args, void* stream
  * (python/dtorch/nn/scaled_dot_product_attention_with_cp.py:87-101); this is the combine step of
  * the blockwise ring.  With m = max_b LSE_b: LSE = m + log sum_b exp(LSE_b - m) and
  * O = sum_b exp(LSE_b - LSE) O_b.  Blocks with LSE = -inf contribute nothing.
- * All blocks share one shape [B, H, S, D] and one set of strides.
+ * All blocks share one shape [B, H, S, D] and one set of strides; D is a multiple of 8 (ABI version 6).
  */
 #define DTATTN_MAX_MERGE_BLOCKS 16
 typedef struct {

@@ -83,8 +83,12 @@ def _last_error():
 
 @pytest.mark.parametrize("kw,code,text", [
     (dict(Hq=6, Hkv=4), 1, "multiple"),
-    (dict(D=96, Dv=96), 2, "head dim"),
-    (dict(Dv=64), 2, "Dv"),
+    (dict(D=100, Dv=100), 2, "multiples of 8"),                      # bf16 head dims: multiples of 8
+    (dict(D=520, Dv=520), 2, "exceeds 512"),
+    (dict(Dv=64, dtype=3, o_dtype=3), 2, "bf16/fp16 only"),           # D != Dv: 16-bit inputs only
+    (dict(D=96, Dv=96, dtype=3, o_dtype=3), 2, "head dim"),          # fp32: 64 or 128
+    (dict(D=96, Dv=96, dtype=2, o_dtype=0, q_descale=0x10000, k_descale=0x10000, v_descale=0x10000), 2,
+     "head dim"),                                                    # fp8: 64 or 128
     (dict(dtype=5, o_dtype=5), 2, "dtype"),
     (dict(dtype=3, o_dtype=0), 2, "output dtype"),                   # fp32 inputs need an fp32 output
     (dict(dtype=3, o_dtype=3, q_stride=(ctypes.c_int64 * 3)(8 * 64 * 128, 64 * 128, 130)), 2, "16 bytes"),
