@@ -9,6 +9,7 @@
 #include <c10/hip/HIPStream.h>
 
 #include <cmath>
+#include <cstring>
 #include <limits>
 #include <sstream>
 #include <stdexcept>
@@ -261,6 +262,14 @@ PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::T
         a.v_stride[0] = v.sb, a.v_stride[1] = v.sh, a.v_stride[2] = v.ss;
         a.dtype = DtypeCode(st);
         a.o_dtype = a.dtype;
+    }
+    // Workspace for the key blocks of small wide-head grids (zero bytes for every other call).
+    at::Tensor wst;
+    const size_t ws = dtattn_prefill_workspace_size(&a);
+    if (ws > 0) {
+        wst = at::empty({(int64_t)ws}, q_.options().dtype(at::kByte));
+        a.workspace = wst.data_ptr();
+        a.workspace_bytes = ws;
     }
     Check(dtattn_prefill_fwd(&a, stream), "dtattn_prefill_fwd");
     if (!ov.t.is_same(o)) o.copy_(ov.t);

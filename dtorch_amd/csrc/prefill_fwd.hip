@@ -26,6 +26,7 @@
 //   O^T += V^T(j) P^T(j)
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
 
 #include "dtattn_common.hpp"
 #include "prefill_params.hpp"
@@ -386,6 +387,38 @@ static int dispatch_prefill(const PrefillParams& p, int D, bool causal, bool pad
 int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_t stream);
 int prefill_f32(const PrefillParams& p, int D, bool causal, hipStream_t stream);
 int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, bool pad, hipStream_t stream);
+int wide_key_splits(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int D, int cu_count);
+
+// Kernel head dim of a bf16/fp16 call: the smallest of 64, 128, 256, 512 holding both real head dims.
+static int kernel_head_dim(int64_t D, int64_t Dv) {
+    const int64_t dmax = D > Dv ? D : Dv;
+    return dmax <= 64 ? 64 : dmax <= 128 ? 128 : dmax <= 256 ? 256 : dmax <= 512 ? 512 : 0;
+}
+
+// Key blocks of a wide-head call on `device` (1: unsplit) and the workspace their partials need:
+// O parts [splits][B][Hq][Sq][Dv] in the input dtype, then (256-byte aligned) LSE parts
+// [splits][B][Hq][Sq] fp32.
+static int wide_plan(const dtattn_prefill_args* a, int device, size_t* bytes, size_t* lse_off) {
+    *bytes = 0;
+    *lse_off = 0;
+    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16) return 1;
+    if (a->D % 8 != 0 || a->Dv % 8 != 0 || a->B <= 0 || a->Sq <= 0 || a->Sk <= 0) return 1;
+    const int Dk = kernel_head_dim(a->D, a->Dv);
+    if (Dk < 256) return 1;
+    dtattn_device_peaks pk;
+    if (dtattn_get_device_peaks(device, &pk) != DTATTN_OK) return 1;
+    const int splits = wide_key_splits(a->B, a->Hq, a->Sq, a->Sk, Dk, pk.cu_count);
+    if (splits <= 1) return 1;
+    const size_t o_bytes = (size_t)splits * a->B * a->Hq * a->Sq * a->Dv * 2;
+    *lse_off = (o_bytes + 255) & ~(size_t)255;
+    *bytes = *lse_off + (size_t)splits * a->B * a->Hq * a->Sq * sizeof(float);
+    return splits;
+}
+
+static int stream_device(hipStream_t stream, int* dev) {
+    return (stream == nullptr ? hipGetDevice(dev) : hipStreamGetDevice(stream, dev)) == hipSuccess ? DTATTN_OK
+                                                                                               : DTATTN_ERR_DEVICE;
+}
 
 static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
@@ -491,6 +524,10 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     p.mask = a->mask;
     p.ms_b = a->mask_stride[0], p.ms_h = a->mask_stride[1], p.ms_l = a->mask_stride[2];
     p.inv_scale = 1.0f / scale;
+    p.nsplit = 1;
+    p.kblock = (int32_t)(a->Sk > 0 ? a->Sk : 1);
+    p.os_split = 0;
+    p.lses_split = 0;
     const bool causal = a->causal != 0;
     if (a->dtype == DTATTN_FP32) {
         p.qk_ch = p.v_ch = (int32_t)(a->D / 4);
@@ -498,14 +535,63 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     }
     // bf16 / fp16: the kernel head dim is the smallest of 64, 128, 256, 512 that holds both real head
     // dims; smaller real dims (multiples of 8, D and Dv independent) run the padded instantiations.
-    const int64_t dmax = a->D > a->Dv ? a->D : a->Dv;
-    const int Dk = dmax <= 64 ? 64 : dmax <= 128 ? 128 : dmax <= 256 ? 256 : dmax <= 512 ? 512 : 0;
+    const int Dk = kernel_head_dim(a->D, a->Dv);
     if (Dk == 0)
-        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %lld exceeds 512", (long long)dmax);
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %lld exceeds 512",
+                    (long long)(a->D > a->Dv ? a->D : a->Dv));
     p.qk_ch = (int32_t)(a->D / 8);
     p.v_ch = (int32_t)(a->Dv / 8);
     const bool pad = a->D != Dk || a->Dv != Dk;
-    if (Dk >= 256) return prefill_wide(p, Dk, causal, a->dtype == DTATTN_BF16, pad, stream);
+    if (Dk >= 256) {
+        int splits = 1;
+        size_t need = 0, lse_off = 0;
+        if (a->workspace != nullptr && a->workspace_bytes > 0 && (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0) {
+            int dev = 0;
+            if (stream_device(stream, &dev) != DTATTN_OK) return fail(DTATTN_ERR_DEVICE, "prefill: stream device");
+            splits = wide_plan(a, dev, &need, &lse_off);
+            if (need > a->workspace_bytes) splits = 1;
+        }
+        if (splits <= 1) return prefill_wide(p, Dk, causal, a->dtype == DTATTN_BF16, pad, stream);
+        // Key blocks in one launch, then their (O, LSE) merged by LSE into the caller's outputs.
+        const int64_t tiles = (a->Sk + 31) / 32;
+        p.kblock = (int32_t)((tiles + splits - 1) / splits * 32);
+        p.nsplit = (int32_t)((a->Sk + p.kblock - 1) / p.kblock);
+        char* ws = static_cast<char*>(a->workspace);
+        p.o = ws;
+        p.os_b = a->Hq * a->Sq * a->Dv, p.os_h = a->Sq * a->Dv, p.os_s = a->Dv;
+        p.os_split = a->B * a->Hq * a->Sq * a->Dv;
+        p.lse = reinterpret_cast<float*>(ws + lse_off);
+        p.lses_b = a->Hq * a->Sq, p.lses_h = a->Sq;
+        p.lses_split = a->B * a->Hq * a->Sq;
+        const int st = prefill_wide(p, Dk, causal, a->dtype == DTATTN_BF16, pad, stream);
+        if (st != DTATTN_OK) return st;
+        dtattn_merge_args m;
+        memset(&m, 0, sizeof(m));
+        m.n_blocks = p.nsplit;
+        for (int i = 0; i < p.nsplit; ++i) {
+            m.o_blocks[i] = ws + (size_t)i * p.os_split * 2;
+            m.lse_blocks[i] = reinterpret_cast<const float*>(ws + lse_off) + (size_t)i * p.lses_split;
+        }
+        m.B = a->B, m.H = a->Hq, m.S = a->Sq, m.D = a->Dv;
+        m.block_o_stride[0] = p.os_b, m.block_o_stride[1] = p.os_h, m.block_o_stride[2] = p.os_s;
+        m.block_lse_stride[0] = p.lses_b, m.block_lse_stride[1] = p.lses_h;
+        m.block_dtype = a->dtype;
+        m.o = a->o;
+        m.o_stride[0] = a->o_stride[0], m.o_stride[1] = a->o_stride[1], m.o_stride[2] = a->o_stride[2];
+        m.lse = a->lse;
+        m.lse_stride[0] = a->lse_stride[0], m.lse_stride[1] = a->lse_stride[1];
+        m.o_dtype = a->o_dtype;
+        return dtattn_lse_merge(&m, stream);
+    }
     if (a->dtype == DTATTN_BF16) return dispatch_prefill<bf16_t>(p, Dk, causal, pad, stream);
     return dispatch_prefill<f16_t>(p, Dk, causal, pad, stream);
+}
+
+extern "C" size_t dtattn_prefill_workspace_size(const dtattn_prefill_args* a) {
+    if (a == nullptr) return 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    size_t bytes = 0, lse_off = 0;
+    wide_plan(a, dev, &bytes, &lse_off);
+    return bytes;
 }

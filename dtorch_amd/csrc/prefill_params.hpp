@@ -33,6 +33,10 @@ struct PrefillParams {
     // v_ch; the chunks past them load as zeros (adding nothing to the scores, giving O columns that are
     // never stored).
     int32_t qk_ch, v_ch;
+    // Key blocks (wide kernel): workgroup (x, y) takes keys [y kblock, (y + 1) kblock) and writes its
+    // partial O and LSE at o + y os_split, lse + y lses_split; nsplit = 1 is the unsplit launch.
+    int32_t nsplit, kblock;
+    int64_t os_split, lses_split;
 };
 
 // Lazy rescaling: the running max only moves (and O, l are only rescaled) when some row's max grew

@@ -1,4 +1,4 @@
-// Attention forward for wide heads (D = 256, 512) on bf16 / fp16 MFMA, with per-row LSE.
+// Attention forward for wide heads (kernel head dims 256, 512) on bf16 / fp16 MFMA, with per-row LSE.
 //
 // The arithmetic of SdpaOp::Compute (dtorch/core/operators/standard/scaled_dot_product_attention_op.cc:
 // 107-109) at head dims where the main kernel's plan (32 query rows per wave, Q and O of the full head
@@ -6,15 +6,20 @@
 // mid-block attention of its diffusers ports: one head of block_out_channels[-1] = 512 dimensions
 // (python/dtorch/applications/huggingface/diffusers/models/unets/unet_2d_blocks.py:126-140).
 //
-// Work decomposition: a workgroup owns 32 query rows of one (batch, query head).  Wave w owns the
-// dimensions [w D/4, (w+1) D/4): it holds Q and accumulates O for that quarter only.
-//   - S^T = K Q^T is a sum over the four quarters: each wave computes its partial 32x32 tile with
-//     v_mfma_f32_32x32x16, writes it to LDS, and after one barrier every wave reads and sums all four.
-//     The softmax of the 32x32 tile is then computed identically by the four waves (16 scores per
-//     lane), so no further exchange is needed.
-//   - O^T = V^T P^T for the wave's quarter, with V^T read by ds_read_b64_tr_b16 as in the main kernel.
-// Key tiles of 32 rows, K and V double-buffered through direct buffer->LDS loads: 128 KB plus the 20 KB
-// exchange at D = 512, 84 KB at D = 256; one workgroup per CU either way.
+// Work decomposition: a workgroup of 2 NRG waves owns 32 NRG query rows of one (batch, query head): NRG
+// row groups of 32 rows, each handled by a pair of waves that split the head dims in halves.  Wave
+// (rg, dh) holds Q and accumulates O for rows 32 rg .. 32 rg + 31 and dims [dh D/2, (dh + 1) D/2):
+//   - S^T = K Q^T is the sum of the pair's two halves: each wave computes its partial 32x32 tile with
+//     v_mfma_f32_32x32x16, writes it to LDS, and after one barrier adds its partner's.  Both waves of
+//     the pair then hold the same scores and run the same softmax, so no further exchange is needed.
+//   - O^T = V^T P^T for the wave's half, with V^T read by ds_read_b64_tr_b16 as in the main kernel.
+// Per 32-key tile a wave reads half of K and V plus one partner partial from LDS: about 40 KB per 32
+// MFMAs at D = 512, against 36 KB per 16 MFMAs when four waves split the score reduction.
+//   D = 256: NRG = 4, 8 waves (two per SIMD, one workgroup per CU), each K/V tile shared by 128 rows;
+//            64 KB of tiles plus a 32 KB exchange.
+//   D = 512: NRG = 2, 4 waves with up to 512 registers each (64 of Q and 128 of O per wave do not fit
+//            the 256 of two waves per SIMD); 128 KB of tiles plus a 16 KB exchange, 64 rows per tile.
+// Key tiles of 32 rows, K and V double-buffered through direct buffer->LDS loads.
 #include "dtattn_common.hpp"
 #include "prefill_params.hpp"
 
@@ -27,17 +32,17 @@ __device__ __forceinline__ int wswz(int r) { return 4 * (r & 3) + ((r >> 2) & 3)
 
 // PAD: real head dims below D (multiples of 8, Dv may differ from D), as in the main kernel: Q/K chunks
 // past p.qk_ch and V chunks past p.v_ch load as zeros, O chunks past p.v_ch are not stored.
-template <typename T, int D, bool CAUSAL, bool MASKED, bool PAD>
-__global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParams p) {
-    constexpr int NW = 4;
+template <typename T, int D, int NRG, bool CAUSAL, bool MASKED, bool PAD>
+__global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const PrefillParams p) {
+    constexpr int NW = 2 * NRG;
     constexpr int BN = 32;           // keys per tile
-    constexpr int BM = 32;           // query rows per workgroup
-    constexpr int DQ = D / NW;       // dimensions per wave
+    constexpr int BM = 32 * NRG;     // query rows per workgroup
+    constexpr int DH = D / 2;        // dimensions per wave
     constexpr int DCH = D / 8;       // 16-byte chunks per row
-    constexpr int KSTEPS = DQ / 16;  // S^T k-steps per wave
-    constexpr int DT = DQ / 32;      // 32-row d tiles of the wave's O^T
-    constexpr int SXP = 20;          // exchange pitch in floats per lane (16 + 4: conflict-free)
+    constexpr int KSTEPS = DH / 16;  // S^T k-steps per wave
+    constexpr int DT = DH / 32;      // 32-row d tiles of the wave's O^T
     static_assert(D == 256 || D == 512, "wide head dims");
+    static_assert(NRG >= 1 && NRG <= 4, "a tile buffer stages each row group's output");
     typedef typename Elem<T>::vec8 V8;
     typedef typename Elem<T>::vec4 V4;
     typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -47,14 +52,18 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
     __shared__ __attribute__((aligned(16))) T Kb[BN * D];
     __shared__ __attribute__((aligned(16))) T Va[BN * D];
     __shared__ __attribute__((aligned(16))) T Vb[BN * D];
-    __shared__ __attribute__((aligned(16))) float Sx[NW * 64 * SXP];
+    // Partial scores, one 64 x 16 fp32 slab per wave; lane l's 16-byte chunk j at l * 16 + 4 (j ^ (l & 3)),
+    // which spreads 16 consecutive lanes over all 64 banks.
+    __shared__ __attribute__((aligned(16))) float Sx[NW * 64 * 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rg = wave >> 1;  // row group
+    const int dh = wave & 1;   // half of the head dims
     const int l32 = lane & 31;
     const int hf = lane >> 5;
-    const int d0 = wave * DQ;  // first dimension of this wave's quarter
+    const int d0 = dh * DH;    // first dimension of this wave's half
 
     const BlockCoord bc = block_coord<CAUSAL>(p);
     const int qb = bc.qb, b = bc.b, hq = bc.hq, hk = bc.hk;
@@ -62,18 +71,24 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
     const T* kp = reinterpret_cast<const T*>(p.k) + b * p.ks_b + hk * p.ks_h;
     const T* vp = reinterpret_cast<const T*>(p.v) + b * p.vs_b + hk * p.vs_h;
     const int q0 = qb * BM;
+    const int wq0 = q0 + rg * 32;  // first row of this wave's row group
 
-    int kend = p.Sk;
+    // Key block of this workgroup (the whole key range unless split): tiles t0 .. nt - 1, indexed from
+    // key 0 so that tile t always holds keys 32 t .. 32 t + 31.
+    const int split = blockIdx.y;
+    const int kb0 = split * p.kblock;
+    int kend = min(p.Sk, kb0 + p.kblock);
     if (CAUSAL) {
         const int lim = q0 + BM + p.delta;  // keys < lim can be visible
-        kend = lim < 0 ? 0 : (lim < p.Sk ? lim : p.Sk);
+        kend = lim < 0 ? 0 : (lim < kend ? lim : kend);
     }
-    const int nt = (kend + BN - 1) / BN;
+    const int t0 = kb0 / BN;
+    const int nt = kend > kb0 ? (kend + BN - 1) / BN : t0;
 
-    // Q fragment of the wave's quarter (B operand of S^T): lane holds query l32, d = d0 + ks*16 + hf*8 .. +8.
+    // Q fragment of the wave's half (B operand of S^T): lane holds query l32, d = d0 + ks*16 + hf*8 .. +8.
     V8 qf[KSTEPS];
     {
-        const int qrow = q0 + l32;
+        const int qrow = wq0 + l32;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             u32x4 raw = {0u, 0u, 0u, 0u};
@@ -93,12 +108,13 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
     const int vrow = (int)(p.vs_s * (int64_t)sizeof(T));
 
     // Tile t -> LDS (lane l -> byte 16*l of a 1 KB block, 1024 / (2 D) rows per instruction), chunk c of
-    // row r at c ^ wswz(r); rows past Sk read zeros, and so do chunks at or past valid_ch (PAD).
+    // row r at c ^ wswz(r); rows past Sk read zeros, and so do chunks at or past valid_ch (PAD).  The
+    // resource ends where the tile's last valid row ends.
     auto dma = [&](T* dst, const T* base, int pitch, int64_t stride, int t, int valid_ch) {
         constexpr int ROWS_PER_INSTR = 1024 / (2 * D);
         constexpr int INSTR = BN / ROWS_PER_INSTR / NW;
+        static_assert(INSTR >= 1, "at least one load per wave");
         const int rows = min(BN, p.Sk - t * BN);
-        // the resource ends where the tile's last valid row ends (its real width under PAD)
         const uint32_t nbytes = (uint32_t)((rows - 1) * pitch + (PAD ? valid_ch * 16 : D * (int)sizeof(T)));
         const auto rs = make_rsrc(base + (int64_t)t * BN * stride, nbytes);
 #pragma unroll
@@ -120,9 +136,11 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
 
     const float* mbase_p = MASKED ? p.mask + b * p.ms_b + hq * p.ms_h : nullptr;
     const auto mrs = make_rsrc(mbase_p, MASKED ? (uint32_t)((((int64_t)(p.Sq - 1) * p.ms_l + p.Sk) * 4)) : 0u);
-    const uint32_t mrow_off = MASKED ? (uint32_t)((int64_t)min(q0 + l32, p.Sq - 1) * p.ms_l * 4) : 0u;
+    const uint32_t mrow_off = MASKED ? (uint32_t)((int64_t)min(wq0 + l32, p.Sq - 1) * p.ms_l * 4) : 0u;
 
-    float* sx_mine = Sx + (wave * 64 + lane) * SXP;
+    float* sx_mine = Sx + (wave * 64 + lane) * 16;
+    const float* sx_partner = Sx + ((wave ^ 1) * 64 + lane) * 16;
+    const int sxs = lane & 3;  // chunk swizzle of this lane's slab
 
     auto tile = [&](const T* Kc, const T* Vc, T* Kn, T* Vn, int t) {
         wait_vmem();
@@ -132,39 +150,49 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
             dma(Vn, vp, vrow, p.vs_s, t + 1, p.v_ch);
         }
         const int kbase = t * BN;
-        const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && (kbase + BN - 1 > q0 + p.delta));
+        // Every row of this row group precedes the tile: the pair skips it together (both waves still
+        // reach the exchange barrier below).
+        const bool skip = CAUSAL && kbase > wq0 + 31 + p.delta;
+        const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && (kbase + BN - 1 > wq0 + p.delta));
         u32x4 mraw[4];
         if constexpr (MASKED) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) mraw[g] = buf_ld16(mrs, mrow_off + (uint32_t)((kbase + 8 * g + 4 * hf) * 4));
         }
-        // partial S^T over this wave's quarter
+        // partial S^T over this wave's half
         f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.f;
+        if (!skip) {
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-            const int r = l32;
-            const int c = (d0 + ks * 16 + hf * 8) >> 3;
-            const V8 a = *reinterpret_cast<const V8*>(Kc + r * D + 8 * (c ^ wswz(r)));
-            s = Elem<T>::mfma32(a, qf[ks], s);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<f32x4*>(sx_mine + 4 * j) = f32x4{s[4 * j], s[4 * j + 1], s[4 * j + 2], s[4 * j + 3]};
-        lds_barrier();  // all four partials written
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const float* src = Sx + (w * 64 + lane) * SXP;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f32x4 x = *reinterpret_cast<const f32x4*>(src + 4 * j);
-                s[4 * j] += x.x, s[4 * j + 1] += x.y, s[4 * j + 2] += x.z, s[4 * j + 3] += x.w;
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                const int r = l32;
+                const int c = (d0 + ks * 16 + hf * 8) >> 3;
+                const V8 a = *reinterpret_cast<const V8*>(Kc + r * D + 8 * (c ^ wswz(r)));
+                s = Elem<T>::mfma32(a, qf[ks], s);
             }
+            // K fragment reads run two MFMAs ahead of their use: at D = 512 the wave holds 64 registers
+            // of Q and 128 of O, so deeper read-ahead would spill
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int i = 0; i < KSTEPS - 2; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<f32x4*>(sx_mine + 4 * (j ^ sxs)) =
+                    f32x4{s[4 * j], s[4 * j + 1], s[4 * j + 2], s[4 * j + 3]};
         }
-        // Element i of s holds key kbase + 8*(i/4) + 4*hf + i%4 of query q0 + l32.
+        lds_barrier();  // every partial written
+        if (skip) return;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(sx_partner + 4 * (j ^ sxs));
+            s[4 * j] += x.x, s[4 * j + 1] += x.y, s[4 * j + 2] += x.z, s[4 * j + 3] += x.w;
+        }
+        // Element i of s holds key kbase + 8*(i/4) + 4*hf + i%4 of query wq0 + l32.
         if constexpr (MASKED) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -177,7 +205,7 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
         }
         if (need_mask) {
             int lim = p.Sk - 1 - kbase;
-            if (CAUSAL) lim = min(lim, q0 + l32 + p.delta - kbase);
+            if (CAUSAL) lim = min(lim, wq0 + l32 + p.delta - kbase);
             lim -= 4 * hf;
 #pragma unroll
             for (int i = 0; i < 16; ++i)
@@ -188,7 +216,7 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
         mx = max_xor32(mx);
         const float mcand = fmaxf(mrow, mx * p.c);
-        if (__any(mcand - mrow > kRescaleThreshold)) {  // wave-uniform (and the same in every wave)
+        if (__any(mcand - mrow > kRescaleThreshold)) {  // wave-uniform (and the same in both waves of the pair)
             const float alpha = fast_exp2(mrow - (mcand == kNegInf ? 0.f : mcand));
             mrow = mcand;
             lrow *= alpha;
@@ -212,7 +240,7 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
             pb[half] = pk;
         }
         lrow = ls;
-        // O^T (this wave's quarter) += V^T P^T: k-step ks covers keys 16 ks .. 16 ks + 15
+        // O^T (this wave's half) += V^T P^T: k-step ks covers keys 16 ks .. 16 ks + 15
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -228,21 +256,31 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
                 oacc[dt] = Elem<T>::mfma32(a, pb[ks], oacc[dt]);
             }
         }
+        // V^T reads (two per MFMA) run one MFMA ahead
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+        for (int i = 0; i < 2 * DT - 1; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     };
 
-    if (nt > 0) {
-        dma(Ka, kp, krow, p.ks_s, 0, p.qk_ch);
-        dma(Va, vp, vrow, p.vs_s, 0, p.v_ch);
+    if (nt > t0) {
+        dma(Ka, kp, krow, p.ks_s, t0, p.qk_ch);
+        dma(Va, vp, vrow, p.vs_s, t0, p.v_ch);
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): Q and tile 0, visibly to the compiler
-    for (int t = 0; t < nt; t += 2) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): Q and the first tile, visibly to the compiler
+    for (int t = t0; t < nt; t += 2) {
         tile(Ka, Va, Kb, Vb, t);
         if (t + 1 < nt) tile(Kb, Vb, Ka, Va, t + 1);
     }
 
-    // Epilogue: every wave stages its quarter of the 32 output rows in Ka (row r, 16-byte chunk c at
-    // c ^ (r % 16)), then all 256 threads store whole rows.
+    // Epilogue: row group rg stages its 32 output rows in tile buffer rg (row r, 16-byte chunk c at
+    // c ^ (r % 16)), each wave its half, then all threads store whole rows.
+    static_assert(32 <= BN, "a tile buffer holds one row group's output rows");
     __syncthreads();
+    T* Os = rg == 0 ? Ka : rg == 1 ? Kb : rg == 2 ? Va : Vb;
     {
         const float l = sum_xor32(lrow);
         const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -255,32 +293,42 @@ __global__ void __launch_bounds__(256, 1) prefill_wide_kernel(const PrefillParam
 #pragma unroll
                 for (int e = 0; e < 4; ++e) o4[e] = Elem<T>::from_f32(oacc[dt][4 * i4 + e] * inv);
                 const int c = (d0 >> 3) + dt * 4 + i4;
-                *reinterpret_cast<V4*>(Ka + row * D + 8 * (c ^ (row & 15)) + 4 * hf) = o4;
+                *reinterpret_cast<V4*>(Os + row * D + 8 * (c ^ (row & 15)) + 4 * hf) = o4;
             }
-        if (wave == 0 && p.lse != nullptr && hf == 0) {
-            const int qrow = q0 + row;
-            if (qrow < p.Sq) p.lse[b * p.lses_b + hq * p.lses_h + qrow] = l > 0.f ? (mrow + __log2f(l)) * kLn2 : kNegInf;
+        if (dh == 0 && p.lse != nullptr && hf == 0) {
+            const int qrow = wq0 + row;
+            if (qrow < p.Sq)
+                p.lse[split * p.lses_split + b * p.lses_b + hq * p.lses_h + qrow] =
+                    l > 0.f ? (mrow + __log2f(l)) * kLn2 : kNegInf;
         }
     }
     __syncthreads();
-    T* op = reinterpret_cast<T*>(p.o) + b * p.os_b + hq * p.os_h;
+    T* op = reinterpret_cast<T*>(p.o) + split * p.os_split + b * p.os_b + hq * p.os_h;
 #pragma unroll
-    for (int it = 0; it < BM * DCH / 256; ++it) {
-        const int id = it * 256 + tid;
-        const int row = id / DCH, c = id % DCH;
+    for (int it = 0; it < BM * DCH / (64 * NW); ++it) {
+        const int id = it * 64 * NW + tid;
+        const int row = id / DCH, c = id % DCH;  // row of the workgroup's BM
         const int qrow = q0 + row;
-        if (qrow < p.Sq && (!PAD || c < p.v_ch)) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Ka + row * D + 8 * (c ^ (row & 15))));
+        const T* src = (row < 32 ? Ka : row < 64 ? Kb : row < 96 ? Va : Vb) + (row & 31) * D;
+        if (qrow < p.Sq && (!PAD || c < p.v_ch))
+            st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(src + 8 * (c ^ (row & 15))));
     }
 }
 
+// Row groups per workgroup: see the kernel's header.
+template <int D>
+constexpr int wide_row_groups() { return D == 512 ? 2 : 4; }
+
 template <typename T, int D, bool CAUSAL, bool MASKED, bool PAD>
 static int launch_wide(const PrefillParams& prm, hipStream_t stream) {
+    constexpr int NRG = wide_row_groups<D>();
     PrefillParams p = prm;
-    p.n_qblocks = (p.Sq + 31) / 32;
+    p.n_qblocks = (p.Sq + 32 * NRG - 1) / (32 * NRG);
     const int64_t grid = (int64_t)p.n_qblocks * p.B * p.Hq;
     if (grid == 0) return DTATTN_OK;
     if (grid > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill grid too large (%lld blocks)", (long long)grid);
-    hipLaunchKernelGGL((prefill_wide_kernel<T, D, CAUSAL, MASKED, PAD>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((prefill_wide_kernel<T, D, NRG, CAUSAL, MASKED, PAD>), dim3((unsigned)grid, (unsigned)p.nsplit),
+                       dim3(64 * 2 * NRG), 0, stream, p);
     return check_launch("prefill_wide_kernel");
 }
 
@@ -304,7 +352,21 @@ static int dispatch_wide(const PrefillParams& p, int D, bool causal, bool pad, h
                              : dispatch_wide_m<T, false, false>(p, D, causal, stream);
 }
 
-// Entry from dtattn_prefill_fwd for kernel head dims 256 / 512 with bf16 or fp16 inputs.
+// Key blocks for a wide-head launch of kernel head dim D: the wide kernel runs one workgroup per CU, so
+// a grid of at most half the CU count runs its keys as blocks of whole 32-key tiles (at least 256 keys,
+// at most 8 blocks), in one launch with the blocks on grid.y, about one full round of workgroups.
+int wide_key_splits(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int D, int cu_count) {
+    const int64_t rows = D == 512 ? 32 * wide_row_groups<512>() : 32 * wide_row_groups<256>();
+    const int64_t wgs = (Sq + rows - 1) / rows * B * Hq;
+    if (wgs <= 0 || cu_count <= 0 || wgs * 2 > cu_count) return 1;
+    int64_t n = cu_count / wgs;
+    n = n < Sk / 256 ? n : Sk / 256;
+    n = n < 8 ? n : 8;
+    return n > 1 ? (int)n : 1;
+}
+
+// Entry from dtattn_prefill_fwd for kernel head dims 256 / 512 with bf16 or fp16 inputs.  p.nsplit and
+// p.kblock are set by the caller (1 and Sk when unsplit).
 int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, bool pad, hipStream_t stream) {
     return bf16 ? dispatch_wide<bf16_t>(p, D, causal, pad, stream) : dispatch_wide<f16_t>(p, D, causal, pad, stream);
 }

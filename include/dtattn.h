@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define DTATTN_ABI_VERSION 6
+#define DTATTN_ABI_VERSION 7
 
 typedef enum {
     DTATTN_OK = 0,
@@ -86,9 +86,18 @@ typedef struct {
      * fill of additive masks), hides the key; a boolean mask is passed as 0 / -inf. */
     const float* mask;
     int64_t mask_stride[3];
+    /* Optional workspace (ABI version 7; NULL / 0: none).  Wide heads (a kernel head dim of 256 or 512)
+     * whose grid would leave CUs idle run the keys as several blocks in one launch and merge them by
+     * LSE; the blocks' partial outputs live here.  dtattn_prefill_workspace_size() says how much a call
+     * can use; with less, the call runs unsplit (same results up to the rounding of the partials). */
+    void* workspace;
+    size_t workspace_bytes;
 } dtattn_prefill_args;
 
 int dtattn_prefill_fwd(const dtattn_prefill_args* args, void* stream);
+/* Workspace bytes dtattn_prefill_fwd can use for `args` on the current device (0 when it would not
+ * split the keys); 256-byte aligned pointers expected. */
+size_t dtattn_prefill_workspace_size(const dtattn_prefill_args* args);
 
 /* Split-KV single-token decode against a padded per-sequence KV cache.
  *

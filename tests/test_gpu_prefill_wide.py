@@ -70,3 +70,35 @@ def test_vae_attention_16k_pixels_sampled_rows():
     ro, rl = orc.sdpa_fwd(host(q[:, :, rows]), host(k), host(v))
     assert max_abs(host(o[:, :, rows]), ro) <= O_TOL_BF16
     assert lse_rel(host(lse[:, :, rows]), rl) <= LSE_TOL
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D,causal,q_offset,dtype", [
+    (1, 1, 1, 4096, 4096, 512, False, 0, torch.bfloat16),   # the 64x64-latent VAE attention: 4 key blocks
+    (1, 2, 2, 1024, 1024, 512, True, 0, torch.bfloat16),    # causal key blocks with their offsets
+    (1, 4, 1, 700, 1500, 256, True, 800, torch.float16),    # GQA 4, causal with a query offset
+    (1, 1, 1, 333, 2000, 320, False, 0, torch.bfloat16),    # padded head dim in key blocks
+    (2, 4, 4, 2048, 2048, 512, False, 0, torch.bfloat16),   # a full grid: no split
+])
+def test_prefill_wide_key_blocks(B, Hq, Hkv, Sq, Sk, D, causal, q_offset, dtype):
+    # Grids smaller than the CU count run the keys as several blocks merged by LSE; every row and the LSE
+    # must match the single-pass oracle.
+    o, lse, ro, rl = _case(B, Hq, Hkv, Sq, Sk, D, causal, dtype=dtype, seed=Sq + D, q_offset=q_offset)
+    assert max_abs(o, ro) <= O_TOL_BF16
+    assert lse_rel(lse, rl) <= LSE_TOL
+
+
+def test_prefill_wide_key_blocks_with_mask_and_sdpa_op():
+    rng = np.random.default_rng(77)
+    keep = rng.random((512, 1800)) < 0.5
+    keep[:, 1799] = True
+    o, lse, ro, rl = _case(1, 2, 2, 512, 1800, 512, False, seed=78, mask=keep)
+    assert max_abs(o, ro) <= O_TOL_BF16
+    assert lse_rel(lse, rl) <= LSE_TOL
+    # the one-output SdpaOp takes the same split (no LSE output requested)
+    q, k, v = (torch.randn(1, 1, 512, 512, device="cuda", dtype=torch.bfloat16) for _ in range(3))
+    o1 = _F().scaled_dot_product_attention(q, k, v, is_causal=True)
+    o2, _ = _F().scaled_dot_product_attention_with_lse(q, k, v, is_causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    ro, _ = orc.sdpa_fwd(host(q), host(k), host(v), is_causal=True)
+    assert max_abs(host(o1), ro) <= O_TOL_BF16

@@ -60,7 +60,8 @@ class PrefillArgs(ctypes.Structure):
                 ("dtype", ctypes.c_int32), ("o_dtype", ctypes.c_int32), ("scale", ctypes.c_float),
                 ("causal", ctypes.c_int32), ("q_offset", ctypes.c_int64), ("k_offset", ctypes.c_int64),
                 ("q_descale", ctypes.c_void_p), ("k_descale", ctypes.c_void_p), ("v_descale", ctypes.c_void_p),
-                ("mask", ctypes.c_void_p), ("mask_stride", ctypes.c_int64 * 3)]
+                ("mask", ctypes.c_void_p), ("mask_stride", ctypes.c_int64 * 3),
+                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
 
 
 def _args(**kw):
