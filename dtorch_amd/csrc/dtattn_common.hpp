@@ -102,6 +102,24 @@ __device__ __forceinline__ uint32_t pack2(float x, float y) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// ---- e4m3fn quantization ----------------------------------------------------------------------
+
+// Per-head absmax scaling: the factor applied before rounding and the descale of a head whose max |x|
+// is m (m = 0: both 1).
+__device__ __forceinline__ float quant_inv(float m) { return m > 0.f ? 448.f / m : 1.f; }
+__device__ __forceinline__ float quant_descale(float m) { return m > 0.f ? m / 448.f : 1.f; }
+
+// Four floats times inv, saturated to +-448 and rounded to nearest even e4m3fn (v_cvt_pk_fp8_f32),
+// packed in one word, first value in the low byte.  The quantizer and the attention kernel that
+// quantizes its own Q both use this, so their codes are identical.
+__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, float inv) {
+    int packed = __builtin_amdgcn_cvt_pk_fp8_f32(fminf(fmaxf(a * inv, -448.f), 448.f),
+                                                 fminf(fmaxf(b * inv, -448.f), 448.f), 0, false);
+    packed = __builtin_amdgcn_cvt_pk_fp8_f32(fminf(fmaxf(c * inv, -448.f), 448.f),
+                                             fminf(fmaxf(d * inv, -448.f), 448.f), packed, true);
+    return (uint32_t)packed;
+}
+
 // ---- raw memory access ------------------------------------------------------------------------
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }

@@ -8,6 +8,7 @@
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <limits>
@@ -200,7 +201,8 @@ PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::T
     if (k_.scalar_type() != st || v_.scalar_type() != st) Throw("query, key and value dtypes differ");
     if (st != c10::ScalarType::BFloat16 && st != c10::ScalarType::Half && st != c10::ScalarType::Float)
         Throw(std::string("dtype ") + c10::toString(st) + " is not supported by the MI355X kernels (bf16, fp16, fp32)");
-    if (fp8 && st != c10::ScalarType::BFloat16) Throw("native_fp8 takes bf16 inputs");
+    if (fp8 && st != c10::ScalarType::BFloat16 && st != c10::ScalarType::Half)
+        Throw("native_fp8 takes bf16 or fp16 inputs");
 
     std::vector<int64_t> oshape = q_.sizes().vec();
     oshape.back() = v_.size(-1);
@@ -233,35 +235,21 @@ PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::T
         for (int i = 0; i < 3; ++i) a.mask_stride[i] = maskf.size(i) > 1 ? maskf.stride(i) : 0;
     }
 
-    at::Tensor q8, k8, v8, qd, kd, vd;
+    a.q = q.t.data_ptr(), a.k = k.t.data_ptr(), a.v = v.t.data_ptr();
+    a.q_stride[0] = q.sb, a.q_stride[1] = q.sh, a.q_stride[2] = q.ss;
+    a.k_stride[0] = k.sb, a.k_stride[1] = k.sh, a.k_stride[2] = k.ss;
+    a.v_stride[0] = v.sb, a.v_stride[1] = v.sh, a.v_stride[2] = v.ss;
+    a.dtype = DtypeCode(st);
+    a.o_dtype = a.dtype;
     if (fp8) {
-        auto quantize = [&](const View4& x, at::Tensor& codes, at::Tensor& desc) {
-            codes = at::empty({x.B, x.H, x.S, x.D}, x.t.options().dtype(at::kFloat8_e4m3fn));
-            desc = at::empty({x.B, x.H}, x.t.options().dtype(at::kFloat));
-            const size_t ws = dtattn_fp8_quantize_workspace_size(x.B, x.H, x.S, x.D);
-            at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, x.t.options().dtype(at::kByte));
-            const int64_t strides[3] = {x.sb, x.sh, x.ss};
-            Check(dtattn_fp8_quantize_per_head(x.t.data_ptr(), DtypeCode(st), x.B, x.H, x.S, x.D, strides,
-                                               codes.data_ptr(), desc.data_ptr<float>(), wst.data_ptr(), ws, stream),
-                  "dtattn_fp8_quantize_per_head");
-        };
-        quantize(q, q8, qd);
-        quantize(k, k8, kd);
-        quantize(v, v8, vd);
-        a.q = q8.data_ptr(), a.k = k8.data_ptr(), a.v = v8.data_ptr();
-        a.q_stride[0] = q.H * q.S * q.D, a.q_stride[1] = q.S * q.D, a.q_stride[2] = q.D;
-        a.k_stride[0] = k.H * k.S * k.D, a.k_stride[1] = k.S * k.D, a.k_stride[2] = k.D;
-        a.v_stride[0] = v.H * v.S * v.D, a.v_stride[1] = v.S * v.D, a.v_stride[2] = v.D;
-        a.dtype = DTATTN_FP8_E4M3FN;
-        a.o_dtype = DTATTN_BF16;
-        a.q_descale = qd.data_ptr<float>(), a.k_descale = kd.data_ptr<float>(), a.v_descale = vd.data_ptr<float>();
-    } else {
-        a.q = q.t.data_ptr(), a.k = k.t.data_ptr(), a.v = v.t.data_ptr();
-        a.q_stride[0] = q.sb, a.q_stride[1] = q.sh, a.q_stride[2] = q.ss;
-        a.k_stride[0] = k.sb, a.k_stride[1] = k.sh, a.k_stride[2] = k.ss;
-        a.v_stride[0] = v.sb, a.v_stride[1] = v.sh, a.v_stride[2] = v.ss;
-        a.dtype = DtypeCode(st);
-        a.o_dtype = a.dtype;
+        // per-head e4m3fn quantization and fp8 attention in one call; the K/V codes live in its workspace
+        const size_t ws = dtattn_prefill_fp8_workspace_size(&a);
+        at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, q_.options().dtype(at::kByte));
+        a.workspace = wst.data_ptr();
+        a.workspace_bytes = ws;
+        Check(dtattn_prefill_fp8(&a, stream), "dtattn_prefill_fp8");
+        if (!ov.t.is_same(o)) o.copy_(ov.t);
+        return {o, lse};
     }
     // Workspace for the key blocks of small wide-head grids (zero bytes for every other call).
     at::Tensor wst;

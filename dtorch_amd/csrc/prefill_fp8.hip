@@ -1,5 +1,10 @@
 // fp8 (OCP e4m3fn) attention forward for gfx950: Q/K/V codes with per-head descales, fp32
-// accumulation on v_mfma_f32_32x32x64_f8f6f4, fp32 online softmax, bf16 output, fp32 LSE.
+// accumulation on v_mfma_f32_32x32x64_f8f6f4, fp32 online softmax, bf16 or fp16 output, fp32 LSE.
+//
+// Two entry points: dtattn_prefill_fwd with FP8 codes from the caller, and dtattn_prefill_fp8, the
+// native fp8 path from bf16/fp16 inputs in three launches: per-head maxima of q, k and v; K/V codes
+// plus the scales of all three; then this kernel, which rounds its own 128 Q rows to e4m3 in registers
+// with the same per-head factor (so Q's codes never go through memory).
 //
 // Supersedes the quantized branch of SdpaOp::Compute, which hands q/k/v to the third-party
 // SageAttention package (dtorch/core/operators/standard/scaled_dot_product_attention_op.cc:110-117,
@@ -17,19 +22,23 @@
 //        as P * 2^7 straight from the score registers, in the same key order.
 //   Dequantisation: logits use scale * log2(e) * dq * dk; the output is acc * dv / l, with the row
 //   sum l accumulated over the same 2^7-scaled P.
+#include <string.h>
+
 #include "dtattn_common.hpp"
+#include "fp8_quant.hpp"
 
 namespace dtattn {
 
 struct PrefillFp8Params {
-    const uint8_t* q;
+    const void* q;  // codes, or bf16/fp16 rows rounded in the kernel (factor qinv)
     const uint8_t* k;
     const uint8_t* v;
-    bf16_t* o;
+    void* o;
     float* lse;
     const float* qd;
     const float* kd;
     const float* vd;
+    const float* qinv;  // [B*Hq] 448 / amax of q's head, for 16-bit q
     int64_t qs_b, qs_h, qs_s;
     int64_t ks_b, ks_h, ks_s;
     int64_t vs_b, vs_h, vs_s;
@@ -56,7 +65,8 @@ __device__ __forceinline__ int fswz(int r) {
     return D >= 128 ? (2 * ((r >> 1) & 3)) ^ ((r >> 5) & 1) : (2 * ((r >> 2) & 1)) ^ ((r >> 5) & 1);
 }
 
-template <int D, bool CAUSAL>
+// TQ: uint8_t (Q given as codes) or bf16_t / f16_t (Q rounded here); TO: the output element type.
+template <int D, bool CAUSAL, typename TQ, typename TO>
 __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Params p) {
     constexpr int NW = 4;
     constexpr int BN = 64;
@@ -83,7 +93,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
     const BlockCoord bc = block_coord<CAUSAL>(p.B, p.Hq, p.Hkv, p.group, p.n_qblocks, p.xcd_map);
     const int qb = bc.qb, b = bc.b, hq = bc.hq, hk = bc.hk;
 
-    const uint8_t* qp = p.q + b * p.qs_b + hq * p.qs_h;
+    const TQ* qp = reinterpret_cast<const TQ*>(p.q) + b * p.qs_b + hq * p.qs_h;
     const uint8_t* kp = p.k + b * p.ks_b + hk * p.ks_h;
     const uint8_t* vp = p.v + b * p.vs_b + hk * p.vs_h;
     const float cq = p.c * p.qd[b * p.Hq + hq] * p.kd[b * p.Hkv + hk];
@@ -103,15 +113,38 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
     i32x8 qf[KSTEPS];
     {
         const int qrow = wq0 + l32;
+        if constexpr (sizeof(TQ) == 1) {
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-            u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-            if (qrow < p.Sq) {
-                const uint8_t* src = qp + (int64_t)qrow * p.qs_s + ks * 64 + hf * 32;
-                lo = ld16(src);
-                hi = ld16(src + 16);
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+                if (qrow < p.Sq) {
+                    const TQ* src = qp + (int64_t)qrow * p.qs_s + ks * 64 + hf * 32;
+                    lo = ld16(src);
+                    hi = ld16(src + 16);
+                }
+                qf[ks] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
             }
-            qf[ks] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        } else {
+            // 16-bit rows rounded to e4m3 with the head's factor, exactly as the quantizer rounds them
+            const float qinv = p.qinv[b * p.Hq + hq];
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                u32x4 raw[4] = {};
+                if (qrow < p.Sq) {
+                    const TQ* src = qp + (int64_t)qrow * p.qs_s + ks * 64 + hf * 32;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) raw[j] = ld16(src + 8 * j);
+                }
+                uint32_t w[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float x[8];
+                    unpack8<TQ>(raw[j], x);
+                    w[2 * j] = quant4(x[0], x[1], x[2], x[3], qinv);
+                    w[2 * j + 1] = quant4(x[4], x[5], x[6], x[7], qinv);
+                }
+                qf[ks] = i32x8{(int)w[0], (int)w[1], (int)w[2], (int)w[3], (int)w[4], (int)w[5], (int)w[6], (int)w[7]};
+            }
         }
     }
 
@@ -258,13 +291,14 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
         if (t + 1 < nt) tile(Kb, Vb, Ka, Va, t + 1);
     }
 
-    // Epilogue: normalise, stage O (bf16) through LDS -- wave w in the 32 x D bf16 slab that is tile
+    // Epilogue: normalise, stage O (16-bit) through LDS -- wave w in the 32 x D slab that is tile
     // buffer w, 16-byte chunk c of row r at c ^ (r % OCH) -- for 16-byte coalesced row stores, and
     // write the LSE.
-    constexpr int OCH = D / 8;  // 16-byte chunks per bf16 output row
+    typedef typename Elem<TO>::vec4 O4;
+    constexpr int OCH = D / 8;  // 16-byte chunks per 16-bit output row
     static_assert(32 * D * 2 <= BN * D, "a tile buffer holds one wave's output rows");
     __syncthreads();
-    bf16_t* Os = reinterpret_cast<bf16_t*>(wave == 0 ? Ka : wave == 1 ? Kb : wave == 2 ? Va : Vb);
+    TO* Os = reinterpret_cast<TO*>(wave == 0 ? Ka : wave == 1 ? Kb : wave == 2 ? Va : Vb);
     {
         const float l = sum_xor32(lrow);
         const float inv = l > 0.f ? vdesc / l : 0.f;
@@ -273,11 +307,11 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
-                bf16x4 o4;
+                O4 o4;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o4[e] = static_cast<bf16_t>(oacc[dt][4 * i4 + e] * inv);
+                for (int e = 0; e < 4; ++e) o4[e] = Elem<TO>::from_f32(oacc[dt][4 * i4 + e] * inv);
                 const int c = dt * 4 + i4;
-                *reinterpret_cast<bf16x4*>(Os + row * D + 8 * (c ^ (row % OCH)) + 4 * hf) = o4;
+                *reinterpret_cast<O4*>(Os + row * D + 8 * (c ^ (row % OCH)) + 4 * hf) = o4;
             }
         if (p.lse != nullptr && hf == 0) {
             const int qrow = wq0 + row;
@@ -288,7 +322,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
         }
     }
     __syncthreads();
-    bf16_t* op = p.o + b * p.os_b + hq * p.os_h;
+    TO* op = reinterpret_cast<TO*>(p.o) + b * p.os_b + hq * p.os_h;
 #pragma unroll
     for (int it = 0; it < 32 * OCH / 64; ++it) {
         const int id = it * 64 + lane;
@@ -298,22 +332,32 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
     }
 }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, typename TQ, typename TO>
 static int launch_fp8(const PrefillFp8Params& prm, hipStream_t stream) {
     PrefillFp8Params p = prm;
     p.n_qblocks = (p.Sq + 127) / 128;
     const int64_t grid = (int64_t)p.n_qblocks * p.B * p.Hq;
     if (grid == 0) return DTATTN_OK;
-    hipLaunchKernelGGL((prefill_fp8_kernel<D, CAUSAL>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    if (grid > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill fp8: grid too large");
+    hipLaunchKernelGGL((prefill_fp8_kernel<D, CAUSAL, TQ, TO>), dim3((unsigned)grid), dim3(256), 0, stream, p);
     return check_launch("prefill_fp8_kernel");
 }
 
-int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_t stream) {
+template <typename TQ, typename TO>
+static int dispatch_fp8(const PrefillFp8Params& p, int64_t D, bool causal, hipStream_t stream) {
+    if (D == 128) return causal ? launch_fp8<128, true, TQ, TO>(p, stream) : launch_fp8<128, false, TQ, TO>(p, stream);
+    if (D == 64) return causal ? launch_fp8<64, true, TQ, TO>(p, stream) : launch_fp8<64, false, TQ, TO>(p, stream);
+    return fail(DTATTN_ERR_UNSUPPORTED, "prefill fp8: head dim %lld not supported (64 or 128)", (long long)D);
+}
+
+// Kernel parameters from the ABI arguments; q/k/v pointers, strides and descales are the caller's.
+static PrefillFp8Params fp8_params(const dtattn_prefill_args* a, float c, int32_t delta) {
     PrefillFp8Params p;
-    p.q = reinterpret_cast<const uint8_t*>(a->q);
+    memset(&p, 0, sizeof(p));
+    p.q = a->q;
     p.k = reinterpret_cast<const uint8_t*>(a->k);
     p.v = reinterpret_cast<const uint8_t*>(a->v);
-    p.o = reinterpret_cast<bf16_t*>(a->o);
+    p.o = a->o;
     p.lse = a->lse;
     p.qd = a->q_descale;
     p.kd = a->k_descale;
@@ -334,10 +378,122 @@ int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_
     p.delta = delta;
     p.c = c;
     p.xcd_map = (p.B * p.Hkv) % 8 == 0 ? 1 : 0;
+    return p;
+}
+
+// dtattn_prefill_fwd with FP8 codes: output BF16 or FP16.
+int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_t stream) {
+    const PrefillFp8Params p = fp8_params(a, c, delta);
     const bool causal = a->causal != 0;
-    if (a->D == 128) return causal ? launch_fp8<128, true>(p, stream) : launch_fp8<128, false>(p, stream);
-    if (a->D == 64) return causal ? launch_fp8<64, true>(p, stream) : launch_fp8<64, false>(p, stream);
-    return fail(DTATTN_ERR_UNSUPPORTED, "prefill fp8: head dim %lld not supported (64 or 128)", (long long)a->D);
+    if (a->o_dtype == DTATTN_FP16) return dispatch_fp8<uint8_t, f16_t>(p, a->D, causal, stream);
+    return dispatch_fp8<uint8_t, bf16_t>(p, a->D, causal, stream);
+}
+
+// Workspace of dtattn_prefill_fp8: K and V codes [B, Hkv, Sk, D], then the per-head scales (q descale and
+// factor, k and v descales) and the slice maxima of the three tensors, each region 256-byte aligned.
+struct Fp8Workspace {
+    size_t k8, v8, qd, qinv, kd, vd, qpart, kpart, vpart, total;
+};
+static Fp8Workspace fp8_workspace(const dtattn_prefill_args* a) {
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    Fp8Workspace w;
+    size_t off = 0;
+    const size_t kv = (size_t)a->B * a->Hkv * a->Sk * a->D;
+    w.k8 = off, off += up(kv);
+    w.v8 = off, off += up(kv);
+    w.qd = off, off += up((size_t)a->B * a->Hq * 4);
+    w.qinv = off, off += up((size_t)a->B * a->Hq * 4);
+    w.kd = off, off += up((size_t)a->B * a->Hkv * 4);
+    w.vd = off, off += up((size_t)a->B * a->Hkv * 4);
+    w.qpart = off, off += up((size_t)a->B * a->Hq * quant_slices(a->Sq) * 4);
+    w.kpart = off, off += up((size_t)a->B * a->Hkv * quant_slices(a->Sk) * 4);
+    w.vpart = off, off += up((size_t)a->B * a->Hkv * quant_slices(a->Sk) * 4);
+    w.total = off;
+    return w;
 }
 
 }  // namespace dtattn
+
+using namespace dtattn;
+
+extern "C" size_t dtattn_prefill_fp8_workspace_size(const dtattn_prefill_args* a) {
+    if (a == nullptr || a->B <= 0 || a->Hq <= 0 || a->Hkv <= 0 || a->Sq < 0 || a->Sk < 0 || a->D <= 0) return 0;
+    return fp8_workspace(a).total;
+}
+
+extern "C" int dtattn_prefill_fp8(const dtattn_prefill_args* a, void* stream_) {
+    if (a == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill_fp8: args is NULL");
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill_fp8: inputs must be bf16 or fp16 (dtype %d)", a->dtype);
+    if (a->o_dtype != a->dtype) return fail(DTATTN_ERR_UNSUPPORTED, "prefill_fp8: output dtype must equal input dtype");
+    if (a->mask != nullptr) return fail(DTATTN_ERR_UNSUPPORTED, "prefill_fp8: an attention mask is not supported");
+    if (a->B < 0 || a->Hq <= 0 || a->Hkv <= 0 || a->Sq < 0 || a->Sk < 0)
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill_fp8: bad sizes");
+    if (a->Hq % a->Hkv != 0) return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill_fp8: Hq is not a multiple of Hkv");
+    if (a->D != a->Dv || (a->D != 64 && a->D != 128))
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill_fp8: head dim %lld / %lld not supported (64 or 128, D == Dv)",
+                    (long long)a->D, (long long)a->Dv);
+    if (a->Sq > (1 << 29) || a->Sk > (1 << 29) || a->B * a->Hq > 65535 || a->B * a->Hkv > 65535)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill_fp8: sizes too large");
+    if (a->B == 0 || a->Sq == 0) return DTATTN_OK;
+    if (a->q == nullptr || a->o == nullptr || (a->Sk > 0 && (a->k == nullptr || a->v == nullptr)))
+        return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill_fp8: null tensor pointer");
+    const int64_t* strides[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
+    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 3; ++j)
+            if ((strides[i][j] * 2) % 16 != 0)
+                return fail(DTATTN_ERR_UNSUPPORTED, "prefill_fp8: strides must be multiples of 16 bytes");
+    if (((reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->k) | reinterpret_cast<uintptr_t>(a->v) |
+          reinterpret_cast<uintptr_t>(a->o)) & 15u) != 0)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill_fp8: tensors must be 16-byte aligned");
+    const Fp8Workspace w = fp8_workspace(a);
+    if (a->workspace == nullptr || a->workspace_bytes < w.total || (reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
+        return fail(DTATTN_ERR_WORKSPACE, "prefill_fp8: a 256-byte aligned workspace of %zu bytes is required, %zu given",
+                    w.total, a->workspace_bytes);
+    char* ws = static_cast<char*>(a->workspace);
+
+    // 1-2. per-head maxima of q, k, v; K/V codes and every scale (q: scales only)
+    QuantParams qp;
+    memset(&qp, 0, sizeof(qp));
+    qp.B = (int32_t)a->B;
+    qp.D = (int32_t)a->D;
+    // tensors q (scales only), k, v; with no keys only q's scales are needed
+    const void* src[3] = {a->q, a->k, a->v};
+    const int64_t* st[3] = {a->q_stride, a->k_stride, a->v_stride};
+    const int64_t H[3] = {a->Hq, a->Hkv, a->Hkv}, S[3] = {a->Sq, a->Sk, a->Sk};
+    const size_t codes[3] = {0, w.k8, w.v8}, desc[3] = {w.qd, w.kd, w.vd}, part[3] = {w.qpart, w.kpart, w.vpart};
+    for (int i = 0; i < 3; ++i) {
+        QuantTensor& t = qp.t[i];
+        t.x = src[i];
+        t.x8 = i > 0 ? reinterpret_cast<uint8_t*>(ws + codes[i]) : nullptr;
+        t.descale = reinterpret_cast<float*>(ws + desc[i]);
+        t.inv = i == 0 ? reinterpret_cast<float*>(ws + w.qinv) : nullptr;
+        t.part = reinterpret_cast<float*>(ws + part[i]);
+        t.xs_b = st[i][0], t.xs_h = st[i][1], t.xs_s = st[i][2];
+        t.H = (int32_t)H[i], t.S = (int32_t)S[i];
+        t.nslice = quant_slices(S[i]);
+    }
+    const int rc = fp8_quantize_batch(qp, a->Sk > 0 ? 3 : 1, a->dtype, stream);
+    if (rc != DTATTN_OK) return rc;
+
+    // 3. attention on the codes, Q rounded in the kernel
+    const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
+    int64_t delta64 = a->q_offset - a->k_offset;
+    const int64_t lim = a->Sq + a->Sk + 1;
+    delta64 = delta64 > lim ? lim : (delta64 < -lim ? -lim : delta64);
+    dtattn_prefill_args codes_args = *a;
+    codes_args.k = ws + w.k8;
+    codes_args.v = ws + w.v8;
+    codes_args.k_stride[0] = a->Hkv * a->Sk * a->D, codes_args.k_stride[1] = a->Sk * a->D, codes_args.k_stride[2] = a->D;
+    codes_args.v_stride[0] = codes_args.k_stride[0], codes_args.v_stride[1] = codes_args.k_stride[1];
+    codes_args.v_stride[2] = a->D;
+    codes_args.q_descale = reinterpret_cast<const float*>(ws + w.qd);
+    codes_args.k_descale = reinterpret_cast<const float*>(ws + w.kd);
+    codes_args.v_descale = reinterpret_cast<const float*>(ws + w.vd);
+    PrefillFp8Params p = fp8_params(&codes_args, scale * kLog2e, (int32_t)delta64);
+    p.qinv = reinterpret_cast<const float*>(ws + w.qinv);
+    const bool causal = a->causal != 0;
+    if (a->dtype == DTATTN_BF16) return dispatch_fp8<bf16_t, bf16_t>(p, a->D, causal, stream);
+    return dispatch_fp8<f16_t, f16_t>(p, a->D, causal, stream);
+}

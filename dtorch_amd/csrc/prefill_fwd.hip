@@ -489,7 +489,8 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
             return fail(DTATTN_ERR_UNSUPPORTED, "prefill: mask slab of one (batch, head) exceeds 4 GB");
     }
     if (a->dtype == DTATTN_FP8_E4M3FN) {
-        if (a->o_dtype != DTATTN_BF16) return fail(DTATTN_ERR_UNSUPPORTED, "prefill fp8: output must be bf16");
+        if (a->o_dtype != DTATTN_BF16 && a->o_dtype != DTATTN_FP16)
+            return fail(DTATTN_ERR_UNSUPPORTED, "prefill fp8: output must be bf16 or fp16");
         if (a->q_descale == nullptr || a->k_descale == nullptr || a->v_descale == nullptr)
             return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill fp8: descale pointers are required");
         return prefill_fp8(a, c, delta, stream);

@@ -52,7 +52,7 @@ typedef enum {
  *
  * dtype: BF16 or FP16 (inputs and output, fp32 softmax and accumulation); FP32 (inputs and output,
  * every step in fp32: the fp32 matrix cores, no 16-bit rounding of P; ABI version 5); or FP8_E4M3FN
- * inputs with descales and a BF16 output.
+ * codes with descales and a BF16 or FP16 (ABI version 7) output.
  * Head dims: BF16/FP16 take any D and Dv that are multiples of 8 up to 512, independently (the output
  * takes v's last axis, as scaled_dot_product_attention_op.cc:26-29 does); the kernels run at 64, 128,
  * 256 or 512 and read the columns past the real dims as zeros (ABI version 6).  FP32 and FP8 take
@@ -98,6 +98,18 @@ int dtattn_prefill_fwd(const dtattn_prefill_args* args, void* stream);
 /* Workspace bytes dtattn_prefill_fwd can use for `args` on the current device (0 when it would not
  * split the keys); 256-byte aligned pointers expected. */
 size_t dtattn_prefill_workspace_size(const dtattn_prefill_args* args);
+
+/* Native fp8 attention from bf16/fp16 inputs (ABI version 7): the path SdpaOption
+ * sageAttentionType "native_fp8" selects, superseding the quantized branch of SdpaOp::Compute that hands
+ * q/k/v to the third-party SageAttention package (dtorch/external/sage_attn/sage_attn_adapter.cc:28-158,
+ * which takes fp16 and bf16).  q, k and v are quantized per (b, head) to e4m3fn as
+ * dtattn_fp8_quantize_per_head does (absmax scaling, round to nearest even), the attention runs on fp8
+ * MFMA with fp32 accumulation, and the output has the inputs' dtype.  args: dtype BF16 or FP16, o_dtype
+ * equal to it, D == Dv in {64, 128}, no mask; `workspace` of dtattn_prefill_fp8_workspace_size() bytes,
+ * 256-byte aligned (K/V codes, scales, partial maxima).  Three launches: the per-head maxima of q, k and
+ * v; the K/V codes and every scale; the attention, which rounds its own Q rows to e4m3 in registers. */
+size_t dtattn_prefill_fp8_workspace_size(const dtattn_prefill_args* args);
+int dtattn_prefill_fp8(const dtattn_prefill_args* args, void* stream);
 
 /* Split-KV single-token decode against a padded per-sequence KV cache.
  *

@@ -131,3 +131,69 @@ def test_fp8_gqa_causal_offsets_ragged(D):
         visible = np.isfinite(dl)
         assert lse_rel(lse[visible], dl[visible]) <= LSE_TOL, (q_off, k_off)
         assert np.all(np.isneginf(lse[~visible])) and np.all(o[~visible] == 0), (q_off, k_off)
+
+
+def _codes_path(q, k, v, causal, dtype, q_offset=0):
+    """The two-step path: the per-head quantizer on q, k, v, then dtattn_prefill_fwd on the FP8 codes
+    through the C ABI, output in `dtype`."""
+    from dtorch_amd import _lib
+    F = _F()
+    (q8, qd), (k8, kd), (v8, vd) = (F.quantize_fp8_per_head(x) for x in (q, k, v))
+    return _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, dtype, causal=causal, q_offset=q_offset)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal,Hq,Hkv,Sq,Sk,D", [(False, 4, 4, 300, 700, 128), (True, 8, 2, 257, 257, 64),
+                                                   (True, 4, 1, 200, 520, 128)])
+def test_fused_fp8_is_bit_identical_to_quantize_then_codes(dtype, causal, Hq, Hkv, Sq, Sk, D):
+    # The fused path rounds Q to e4m3 inside the attention kernel with the quantizer's own per-head factor;
+    # its output and LSE must equal the quantizer + codes path bit for bit.
+    g = torch.Generator(device="cuda").manual_seed(Sq + D)
+    q = (torch.randn(2, Hq, Sq, D, generator=g, device="cuda") * 3).to(dtype)
+    k = torch.randn(2, Hkv, Sk, D, generator=g, device="cuda").to(dtype)
+    v = torch.randn(2, Hkv, Sk, D, generator=g, device="cuda").to(dtype)
+    F = _F()
+    opt = F.SdpaOption(sage_attn_type="native_fp8")
+    qo = 60 if causal else 0
+    o, lse = F.scaled_dot_product_attention_with_lse(q, k, v, is_causal=causal, enable_gqa=Hq != Hkv, q_offset=qo,
+                                                     sdpa_option=opt)
+    ro, rl = _codes_path(q, k, v, causal, dtype, q_offset=qo)
+    torch.cuda.synchronize()
+    assert o.dtype == dtype
+    assert torch.equal(o, ro) and torch.equal(lse, rl)
+
+
+def test_native_fp8_fp16_inputs_against_the_oracle():
+    # fp16 inputs give an fp16 output (the reference's quantized branch takes fp16 and bf16,
+    # sage_attn_adapter.cc:28-40); parity as for bf16 against the dequantized-input oracle
+    rng = np.random.default_rng(16)
+    q, k, v = (randn(rng, (1, 3, 600, 128)) for _ in range(3))
+    F = _F()
+    opt = F.SdpaOption(sage_attn_type="native_fp8")
+    o, lse = F.scaled_dot_product_attention_with_lse(to_dev(q, torch.float16), to_dev(k, torch.float16),
+                                                     to_dev(v, torch.float16), sdpa_option=opt)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float16
+    deq = [orc.fp8_dequantize_per_head(*orc.fp8_quantize_per_head(rounded(x, torch.float16).astype(np.float32)))
+           for x in (q, k, v)]
+    do, dl = orc.sdpa_fwd(*deq)
+    assert max_abs(host(o), do) <= O_TOL_FP8_KERNEL
+    assert lse_rel(host(lse), dl) <= LSE_TOL
+    ro, _ = orc.sdpa_fwd(rounded(q, torch.float16), rounded(k, torch.float16), rounded(v, torch.float16))
+    assert max_abs(host(o), ro) <= O_TOL_FP8
+
+
+def test_native_fp8_empty_keys_and_errors():
+    F = _F()
+    opt = F.SdpaOption(sage_attn_type="native_fp8")
+    q = torch.randn(1, 2, 50, 128, device="cuda", dtype=torch.bfloat16)
+    kv = torch.empty(1, 2, 0, 128, device="cuda", dtype=torch.bfloat16)
+    o, lse = F.scaled_dot_product_attention_with_lse(q, kv, kv, sdpa_option=opt)
+    torch.cuda.synchronize()
+    assert bool((o == 0).all()) and bool(torch.isneginf(lse).all())
+    x = torch.randn(1, 2, 16, 96, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="head dim"):
+        F.scaled_dot_product_attention(x, x, x, sdpa_option=opt)
+    y = torch.randn(1, 2, 16, 128, device="cuda", dtype=torch.float32)
+    with pytest.raises(ValueError, match="bf16 or fp16"):
+        F.scaled_dot_product_attention(y, y, y, sdpa_option=opt)

@@ -49,19 +49,7 @@ def test_abi_version_matches_header():
     assert lib.dtattn_abi_version() == ver == host.abi_version()
 
 
-# ---- ctypes mirror of dtattn_prefill_args (only used for validation paths)
-class PrefillArgs(ctypes.Structure):
-    _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("o", ctypes.c_void_p),
-                ("lse", ctypes.c_void_p),
-                ("B", ctypes.c_int64), ("Hq", ctypes.c_int64), ("Hkv", ctypes.c_int64), ("Sq", ctypes.c_int64),
-                ("Sk", ctypes.c_int64), ("D", ctypes.c_int64), ("Dv", ctypes.c_int64),
-                ("q_stride", ctypes.c_int64 * 3), ("k_stride", ctypes.c_int64 * 3), ("v_stride", ctypes.c_int64 * 3),
-                ("o_stride", ctypes.c_int64 * 3), ("lse_stride", ctypes.c_int64 * 2),
-                ("dtype", ctypes.c_int32), ("o_dtype", ctypes.c_int32), ("scale", ctypes.c_float),
-                ("causal", ctypes.c_int32), ("q_offset", ctypes.c_int64), ("k_offset", ctypes.c_int64),
-                ("q_descale", ctypes.c_void_p), ("k_descale", ctypes.c_void_p), ("v_descale", ctypes.c_void_p),
-                ("mask", ctypes.c_void_p), ("mask_stride", ctypes.c_int64 * 3),
-                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
+PrefillArgs = _lib.PrefillArgs  # ctypes mirror of dtattn_prefill_args (only used for validation paths)
 
 
 def _args(**kw):
