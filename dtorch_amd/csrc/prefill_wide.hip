@@ -52,8 +52,9 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
     __shared__ __attribute__((aligned(16))) T Kb[BN * D];
     __shared__ __attribute__((aligned(16))) T Va[BN * D];
     __shared__ __attribute__((aligned(16))) T Vb[BN * D];
-    // Partial scores, one 64 x 16 fp32 slab per wave; lane l's 16-byte chunk j at l * 16 + 4 (j ^ (l & 3)),
-    // which spreads 16 consecutive lanes over all 64 banks.
+    // Partial scores, one 64 x 16 fp32 slab per wave; lane l's 16-byte chunk j at l * 16 + 4 (j ^ ((l >> 2) & 3)).
+    // Lane l's slab starts on bank 16 (l & 3), so the XOR with bits 2-3 of the lane index puts the 16 lanes
+    // of one 16-byte access pass on 16 distinct 16-byte bank groups.
     __shared__ __attribute__((aligned(16))) float Sx[NW * 64 * 16];
 
     const int tid = threadIdx.x;
@@ -140,7 +141,7 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
 
     float* sx_mine = Sx + (wave * 64 + lane) * 16;
     const float* sx_partner = Sx + ((wave ^ 1) * 64 + lane) * 16;
-    const int sxs = lane & 3;  // chunk swizzle of this lane's slab
+    const int sxs = (lane >> 2) & 3;  // chunk swizzle of this lane's slab
 
     auto tile = [&](const T* Kc, const T* Vc, T* Kn, T* Vn, int t) {
         wait_vmem();
@@ -171,15 +172,15 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
                 const V8 a = *reinterpret_cast<const V8*>(Kc + r * D + 8 * (c ^ wswz(r)));
                 s = Elem<T>::mfma32(a, qf[ks], s);
             }
-            // K fragment reads run two MFMAs ahead of their use: at D = 512 the wave holds 64 registers
-            // of Q and 128 of O, so deeper read-ahead would spill
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            // K fragment reads run four MFMAs ahead of their use: at D = 512 the wave runs alone on its
+            // SIMD, so an LDS read that has not returned stalls the matrix pipe (two ahead: 8% slower)
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-            for (int i = 0; i < KSTEPS - 2; ++i) {
+            for (int i = 0; i < KSTEPS - 4; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 *reinterpret_cast<f32x4*>(sx_mine + 4 * (j ^ sxs)) =
@@ -256,14 +257,16 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
                 oacc[dt] = Elem<T>::mfma32(a, pb[ks], oacc[dt]);
             }
         }
-        // V^T reads (two per MFMA) run one MFMA ahead
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        // V^T reads (two per MFMA) run two MFMAs ahead (one ahead: 8% slower at D = 512, 6-9% at D = 256;
+        // three ahead: no faster).  Spreading the exponentials of P chunk 1 over these MFMAs measured
+        // 4-7% slower than computing P first.
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-        for (int i = 0; i < 2 * DT - 1; ++i) {
+        for (int i = 0; i < 2 * DT - 2; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     };
 
     if (nt > t0) {
