@@ -71,7 +71,7 @@ typedef struct {
     int64_t o_stride[3];
     int64_t lse_stride[2]; /* B, H (S stride is 1) */
     int32_t dtype;   /* dtattn_dtype of q, k, v */
-    int32_t o_dtype; /* dtattn_dtype of o: equal to dtype, or BF16 when dtype is FP8_E4M3FN */
+    int32_t o_dtype; /* dtattn_dtype of o: equal to dtype, or BF16 / FP16 when dtype is FP8_E4M3FN */
     float scale;     /* softmax scale; <= 0 means 1/sqrt(D) */
     int32_t causal;
     int64_t q_offset, k_offset;
