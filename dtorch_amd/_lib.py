@@ -50,7 +50,7 @@ def cabi() -> ctypes.CDLL:
 # ctypes mirrors of the C ABI's argument structs (include/dtattn.h), for callers that drive the library
 # directly: the codes entry point of the fp8 path, the allocation-free decode, tests of the ABI itself.
 class PrefillArgs(ctypes.Structure):
-    """dtattn_prefill_args (ABI version 7)."""
+    """dtattn_prefill_args (ABI version 8); `scale` starts as NaN, the ABI's "1/sqrt(D)"."""
     _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("o", ctypes.c_void_p),
                 ("lse", ctypes.c_void_p),
                 ("B", ctypes.c_int64), ("Hq", ctypes.c_int64), ("Hkv", ctypes.c_int64), ("Sq", ctypes.c_int64),
@@ -63,9 +63,14 @@ class PrefillArgs(ctypes.Structure):
                 ("mask", ctypes.c_void_p), ("mask_stride", ctypes.c_int64 * 3),
                 ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
 
+    def __init__(self, *args, **kw):
+        super().__init__(*args, **kw)
+        if "scale" not in kw:
+            self.scale = float("nan")
+
 
 class DecodeArgs(ctypes.Structure):
-    """dtattn_decode_args."""
+    """dtattn_decode_args (ABI version 8); `scale` starts as NaN, the ABI's "1/sqrt(D)"."""
     _fields_ = [("q", ctypes.c_void_p), ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
                 ("lengths", ctypes.c_void_p), ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p),
                 ("B", ctypes.c_int64), ("Hq", ctypes.c_int64), ("Hkv", ctypes.c_int64), ("S_max", ctypes.c_int64),
@@ -74,6 +79,11 @@ class DecodeArgs(ctypes.Structure):
                 ("o_stride", ctypes.c_int64 * 2), ("lse_stride", ctypes.c_int64 * 1),
                 ("dtype", ctypes.c_int32), ("scale", ctypes.c_float), ("chunk", ctypes.c_int32),
                 ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t)]
+
+    def __init__(self, *args, **kw):
+        super().__init__(*args, **kw)
+        if "scale" not in kw:
+            self.scale = float("nan")
 
 
 def prefill_fp8_codes(q8, k8, v8, qd, kd, vd, out_dtype, causal=False, q_offset=0, k_offset=0, scale=None):
@@ -92,7 +102,7 @@ def prefill_fp8_codes(q8, k8, v8, qd, kd, vd, out_dtype, causal=False, q_offset=
         dst[0], dst[1], dst[2] = t.stride(0), t.stride(1), t.stride(2)
     a.lse_stride[0], a.lse_stride[1] = lse.stride(0), lse.stride(1)
     a.dtype, a.o_dtype = 2, 0 if out_dtype == torch.bfloat16 else 1
-    a.scale = 0.0 if scale is None else float(scale)
+    a.scale = float("nan") if scale is None else float(scale)
     a.causal, a.q_offset, a.k_offset = int(causal), int(q_offset), int(k_offset)
     a.q_descale, a.k_descale, a.v_descale = qd.data_ptr(), kd.data_ptr(), vd.data_ptr()
     lib = cabi()

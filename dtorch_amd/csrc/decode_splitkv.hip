@@ -45,6 +45,7 @@ struct DecodeParams {
     int32_t page_shift, num_pages;
     // real head dim (<= the kernel's D; a multiple of 16 bytes of elements) and its 16-byte chunks
     int32_t d_real, d_ch;
+    uint32_t q_and, q_xor;  // applied to q's words at load, as in ScalePlan
 };
 
 constexpr int kDecodeChunk = 128;  // smallest split; workspace queries with chunk 0 size for it
@@ -126,7 +127,7 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     u32x4 qv[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        qv[g] = ld16(reinterpret_cast<const T*>(p.q) + b * p.qs_b + (hq0 + g) * p.qs_h + c8 * EPC);
+        qv[g] = q_bits(ld16(reinterpret_cast<const T*>(p.q) + b * p.qs_b + (hq0 + g) * p.qs_h + c8 * EPC), p.q_and, p.q_xor);
         if (!cvalid) qv[g] = u32x4{0u, 0u, 0u, 0u};
     }
 
@@ -529,8 +530,12 @@ static int decode_splitkv_run(const dtattn_decode_args* a, void* ws, size_t ws_b
     p.group = (int32_t)(a->Hq / a->Hkv);
     p.chunk = chunk;
     p.nsplit = (int32_t)nsplit;
-    const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
-    p.c = scale * kLog2e;
+    ScalePlan sp;
+    const int sst = plan_scale(a->scale, a->D, a->dtype == DTATTN_FP32 ? kSign32 : kSign16, &sp);
+    if (sst != DTATTN_OK) return sst;
+    p.c = sp.scale * kLog2e;
+    p.q_and = sp.q_and;
+    p.q_xor = sp.q_xor;
     p.block_table = nullptr;
     p.bt_s = 0;
     p.page_shift = 0;
@@ -617,8 +622,12 @@ extern "C" int dtattn_decode_paged(const dtattn_decode_paged_args* a, void* stre
     p.group = (int32_t)(a->Hq / a->Hkv);
     p.chunk = chunk;
     p.nsplit = (int32_t)nsplit;
-    const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
-    p.c = scale * kLog2e;
+    ScalePlan sp;
+    const int sst = plan_scale(a->scale, a->D, a->dtype == DTATTN_FP32 ? kSign32 : kSign16, &sp);
+    if (sst != DTATTN_OK) return sst;
+    p.c = sp.scale * kLog2e;
+    p.q_and = sp.q_and;
+    p.q_xor = sp.q_xor;
     p.block_table = a->block_table;
     p.bt_s = a->block_table_stride;
     p.page_shift = __builtin_ctzll((unsigned long long)a->page_size);

@@ -1,9 +1,11 @@
 // ABI utilities: thread-local error text, launch checks, ABI version and the device peak table.
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
+#include <math.h>
 #include <stdio.h>
 #include <string.h>
 
+#include <cmath>
 #include <mutex>
 
 #include "dtattn_common.hpp"
@@ -30,6 +32,21 @@ int fail(int code, const char* fmt, ...) {
 int check_launch(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(DTATTN_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+    return DTATTN_OK;
+}
+
+// torch::scaled_dot_product_attention takes any scale (scaled_dot_product_attention_op.cc:107-109 forwards
+// SdpaParam's std::optional<double>): logits = scale * q.k (+ mask).  With q negated the logits of
+// |scale| are those of a negative scale; with q zeroed every logit is 0 (+ mask), as at scale 0.
+int plan_scale(float scale, int64_t D, uint32_t sign_bits, ScalePlan* out) {
+    if (std::isnan(scale)) {
+        *out = ScalePlan{1.0f / sqrtf((float)D), 0xffffffffu, 0u};
+        return DTATTN_OK;
+    }
+    if (std::isinf(scale)) return fail(DTATTN_ERR_INVALID_ARGUMENT, "scale must be finite (NaN selects 1/sqrt(D))");
+    if (scale > 0.f) *out = ScalePlan{scale, 0xffffffffu, 0u};
+    else if (scale < 0.f) *out = ScalePlan{-scale, 0xffffffffu, sign_bits};
+    else *out = ScalePlan{1.0f, 0u, 0u};
     return DTATTN_OK;
 }
 

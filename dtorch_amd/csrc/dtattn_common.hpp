@@ -279,6 +279,11 @@ __device__ __forceinline__ float max_across_groups(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// q's 16 bytes after the call's scale plan (see ScalePlan).
+__device__ __forceinline__ u32x4 q_bits(u32x4 w, uint32_t q_and, uint32_t q_xor) {
+    return u32x4{(w.x & q_and) ^ q_xor, (w.y & q_and) ^ q_xor, (w.z & q_and) ^ q_xor, (w.w & q_and) ^ q_xor};
+}
+
 // Workgroup barrier for LDS producer/consumer hand-offs: waits only for this wave's LDS operations
 // (lgkmcnt) before s_barrier.  __syncthreads() is a workgroup release fence, which on gfx9 also
 // drains every outstanding global load (vmcnt(0)) and so would stall prefetches in flight.  The
@@ -333,5 +338,19 @@ __device__ __forceinline__ BlockCoord block_coord(int B, int Hq, int Hkv, int gr
 void set_last_error(const char* fmt, ...);
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
+
+// ---- softmax scale -------------------------------------------------------------------------------
+
+// Sign bits of one 32-bit word of q's elements, by element width.
+constexpr uint32_t kSign16 = 0x80008000u, kSign32 = 0x80000000u, kSign8 = 0x80808080u;
+
+// The softmax scale of a call (a NaN scale selects 1/sqrt(D)), as the kernels run it: always positive.
+// A negative scale runs as |scale| on negated q, zero as scale 1 on zeroed q (every logit is then the
+// mask alone, or 0).  Both are exact bit operations on each 32-bit word of q: (w & q_and) ^ q_xor.
+struct ScalePlan {
+    float scale;
+    uint32_t q_and, q_xor;
+};
+int plan_scale(float scale, int64_t D, uint32_t sign_bits, ScalePlan* out);
 
 }  // namespace dtattn

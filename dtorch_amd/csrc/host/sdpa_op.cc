@@ -187,7 +187,7 @@ PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::T
         if (!prm.enableGqa) Throw("query and key/value head counts differ; set enable_gqa=True");
         if (hq % hkv != 0) Throw("number of query heads must be a multiple of key/value heads");
     }
-    if (prm.scale.has_value() && !(prm.scale.value() > 0.0)) Throw("scale must be positive");
+    if (prm.scale.has_value() && !std::isfinite(prm.scale.value())) Throw("scale must be finite");
 
     std::string quant;
     if (prm.option.has_value()) quant = prm.option->sageAttentionType;
@@ -224,7 +224,7 @@ PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::T
         a.lse = lse.data_ptr<float>();
         a.lse_stride[0] = q.H * q.S, a.lse_stride[1] = q.S;
     }
-    a.scale = prm.scale.has_value() ? (float)prm.scale.value() : 0.f;
+    a.scale = prm.scale.has_value() ? (float)prm.scale.value() : std::nanf("");  // NaN: 1/sqrt(D)
     a.causal = prm.isCausal ? 1 : 0;
     a.q_offset = qOffset, a.k_offset = kOffset;
     at::Tensor maskf;
@@ -362,7 +362,7 @@ void SdpaDecodeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& 
     const c10::ScalarType st = q.scalar_type();
     if (kc.scalar_type() != st || vc.scalar_type() != st) Throw("query and cache dtypes differ");
     if (st != at::kBFloat16 && st != at::kHalf && st != at::kFloat) Throw("decode supports bf16, fp16 and fp32");
-    if (mParam.scale.has_value() && !(mParam.scale.value() > 0.0)) Throw("scale must be positive");
+    if (mParam.scale.has_value() && !std::isfinite(mParam.scale.value())) Throw("scale must be finite");
 
     at::Tensor o = at::empty(q.sizes(), q.options());
     at::Tensor lse = at::empty({q.size(0), q.size(1)}, q.options().dtype(at::kFloat));
@@ -385,7 +385,7 @@ void SdpaDecodeOp::Compute(const TorchTensorOptArray& inputs, TorchTensorArray& 
     a.o_stride[0] = q.size(1) * q.size(3), a.o_stride[1] = q.size(3);
     a.lse_stride[0] = q.size(1);
     a.dtype = DtypeCode(st);
-    a.scale = mParam.scale.has_value() ? (float)mParam.scale.value() : 0.f;
+    a.scale = mParam.scale.has_value() ? (float)mParam.scale.value() : std::nanf("");  // NaN: 1/sqrt(D)
     a.chunk = mParam.chunk;
     const size_t ws = dtattn_decode_workspace_size(a.B, a.Hq, a.S_max, a.D, a.chunk);
     at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, q.options().dtype(at::kByte));
@@ -517,7 +517,7 @@ void SdpaDecodePagedOp::Compute(const TorchTensorOptArray& inputs, TorchTensorAr
     const c10::ScalarType st = q.scalar_type();
     if (kp.scalar_type() != st || vp.scalar_type() != st) Throw("query and page dtypes differ");
     if (st != at::kBFloat16 && st != at::kHalf && st != at::kFloat) Throw("decode supports bf16, fp16 and fp32");
-    if (mParam.scale.has_value() && !(mParam.scale.value() > 0.0)) Throw("scale must be positive");
+    if (mParam.scale.has_value() && !std::isfinite(mParam.scale.value())) Throw("scale must be finite");
     if (kp.stride(3) != 1 || vp.stride(3) != 1) Throw("page pools need a unit stride along D");
 
     at::Tensor o = at::empty(q.sizes(), q.options());
@@ -545,7 +545,7 @@ void SdpaDecodePagedOp::Compute(const TorchTensorOptArray& inputs, TorchTensorAr
     a.lse_stride[0] = q.size(1);
     a.block_table_stride = btc.stride(0);
     a.dtype = DtypeCode(st);
-    a.scale = mParam.scale.has_value() ? (float)mParam.scale.value() : 0.f;
+    a.scale = mParam.scale.has_value() ? (float)mParam.scale.value() : std::nanf("");  // NaN: 1/sqrt(D)
     a.chunk = mParam.chunk;
     const size_t ws = dtattn_decode_paged_workspace_size(a.B, a.Hq, a.max_pages, a.page_size, a.D, a.chunk);
     at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, q.options().dtype(at::kByte));

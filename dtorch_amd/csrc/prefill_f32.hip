@@ -74,7 +74,7 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(const PrefillParams
 #pragma unroll
         for (int g = 0; g < HD / 4; ++g) {
             u32x4 raw = {0u, 0u, 0u, 0u};
-            if (qrow < p.Sq) raw = ld16(qp + (int64_t)qrow * p.qs_s + HD * hf + 4 * g);
+            if (qrow < p.Sq) raw = q_bits(ld16(qp + (int64_t)qrow * p.qs_s + HD * hf + 4 * g), p.q_and, p.q_xor);
             const f32x4 x = __builtin_bit_cast(f32x4, raw);
             qf[4 * g + 0] = x.x, qf[4 * g + 1] = x.y, qf[4 * g + 2] = x.z, qf[4 * g + 3] = x.w;
         }

@@ -49,6 +49,7 @@ struct PrefillFp8Params {
     int32_t delta;
     float c;
     int32_t xcd_map;
+    uint32_t q_and, q_xor;  // applied to q's words at load (codes or 16-bit rows), as in ScalePlan
 };
 
 // P enters the PV MFMA as e4m3 codes of P * 2^kPScaleLog2.  With lazy rescaling P can exceed 1 by up
@@ -119,8 +120,8 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
                 u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
                 if (qrow < p.Sq) {
                     const TQ* src = qp + (int64_t)qrow * p.qs_s + ks * 64 + hf * 32;
-                    lo = ld16(src);
-                    hi = ld16(src + 16);
+                    lo = q_bits(ld16(src), p.q_and, p.q_xor);
+                    hi = q_bits(ld16(src + 16), p.q_and, p.q_xor);
                 }
                 qf[ks] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
             }
@@ -133,7 +134,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
                 if (qrow < p.Sq) {
                     const TQ* src = qp + (int64_t)qrow * p.qs_s + ks * 64 + hf * 32;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) raw[j] = ld16(src + 8 * j);
+                    for (int j = 0; j < 4; ++j) raw[j] = q_bits(ld16(src + 8 * j), p.q_and, p.q_xor);
                 }
                 uint32_t w[8];
 #pragma unroll
@@ -378,12 +379,17 @@ static PrefillFp8Params fp8_params(const dtattn_prefill_args* a, float c, int32_
     p.delta = delta;
     p.c = c;
     p.xcd_map = (p.B * p.Hkv) % 8 == 0 ? 1 : 0;
+    p.q_and = 0xffffffffu;
+    p.q_xor = 0u;
     return p;
 }
 
 // dtattn_prefill_fwd with FP8 codes: output BF16 or FP16.
-int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_t stream) {
-    const PrefillFp8Params p = fp8_params(a, c, delta);
+int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, uint32_t q_and, uint32_t q_xor,
+                hipStream_t stream) {
+    PrefillFp8Params p = fp8_params(a, c, delta);
+    p.q_and = q_and;
+    p.q_xor = q_xor;
     const bool causal = a->causal != 0;
     if (a->o_dtype == DTATTN_FP16) return dispatch_fp8<uint8_t, f16_t>(p, a->D, causal, stream);
     return dispatch_fp8<uint8_t, bf16_t>(p, a->D, causal, stream);
@@ -478,7 +484,10 @@ extern "C" int dtattn_prefill_fp8(const dtattn_prefill_args* a, void* stream_) {
     if (rc != DTATTN_OK) return rc;
 
     // 3. attention on the codes, Q rounded in the kernel
-    const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
+    ScalePlan sp;
+    const int sst = plan_scale(a->scale, a->D, kSign16, &sp);  // q is rounded from its 16-bit rows
+    if (sst != DTATTN_OK) return sst;
+    const float scale = sp.scale;
     int64_t delta64 = a->q_offset - a->k_offset;
     const int64_t lim = a->Sq + a->Sk + 1;
     delta64 = delta64 > lim ? lim : (delta64 < -lim ? -lim : delta64);
@@ -493,6 +502,8 @@ extern "C" int dtattn_prefill_fp8(const dtattn_prefill_args* a, void* stream_) {
     codes_args.v_descale = reinterpret_cast<const float*>(ws + w.vd);
     PrefillFp8Params p = fp8_params(&codes_args, scale * kLog2e, (int32_t)delta64);
     p.qinv = reinterpret_cast<const float*>(ws + w.qinv);
+    p.q_and = sp.q_and;
+    p.q_xor = sp.q_xor;
     const bool causal = a->causal != 0;
     if (a->dtype == DTATTN_BF16) return dispatch_fp8<bf16_t, bf16_t>(p, a->D, causal, stream);
     return dispatch_fp8<f16_t, f16_t>(p, a->D, causal, stream);

@@ -98,7 +98,8 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             u32x4 raw = {0u, 0u, 0u, 0u};
-            if (qrow < p.Sq && (!PAD || 2 * ks + hf < p.qk_ch)) raw = ld16(qp + (int64_t)qrow * p.qs_s + ks * 16 + hf * 8);
+            if (qrow < p.Sq && (!PAD || 2 * ks + hf < p.qk_ch))
+                raw = q_bits(ld16(qp + (int64_t)qrow * p.qs_s + ks * 16 + hf * 8), p.q_and, p.q_xor);
             qf[ks] = __builtin_bit_cast(V8, raw);
         }
     }
@@ -384,7 +385,8 @@ static int dispatch_prefill(const PrefillParams& p, int D, bool causal, bool pad
                              : dispatch_prefill_m<T, false, false>(p, D, causal, stream);
 }
 
-int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, hipStream_t stream);
+int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, uint32_t q_and, uint32_t q_xor,
+                hipStream_t stream);
 int prefill_f32(const PrefillParams& p, int D, bool causal, hipStream_t stream);
 int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, bool pad, hipStream_t stream);
 int wide_key_splits(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int D, int cu_count);
@@ -467,7 +469,13 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     // key/value tiles are addressed with 32-bit byte offsets: 64 rows x row pitch < 2^31
     if (a->k_stride[2] * esz_in * 64 >= (int64_t)1 << 31 || a->v_stride[2] * esz_in * 64 >= (int64_t)1 << 31)
         return fail(DTATTN_ERR_UNSUPPORTED, "prefill: key/value row pitch exceeds 32 MB");
-    const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
+    ScalePlan sp;
+    {
+        const uint32_t sign = a->dtype == DTATTN_FP32 ? kSign32 : a->dtype == DTATTN_FP8_E4M3FN ? kSign8 : kSign16;
+        const int st = plan_scale(a->scale, a->D, sign, &sp);
+        if (st != DTATTN_OK) return st;
+    }
+    const float scale = sp.scale;
     const float c = scale * kLog2e;
     int64_t delta64 = a->q_offset - a->k_offset;
     const int64_t lim = a->Sq + a->Sk + 1;
@@ -493,7 +501,7 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
             return fail(DTATTN_ERR_UNSUPPORTED, "prefill fp8: output must be bf16 or fp16");
         if (a->q_descale == nullptr || a->k_descale == nullptr || a->v_descale == nullptr)
             return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill fp8: descale pointers are required");
-        return prefill_fp8(a, c, delta, stream);
+        return prefill_fp8(a, c, delta, sp.q_and, sp.q_xor, stream);
     }
     if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16 && a->dtype != DTATTN_FP32)
         return fail(DTATTN_ERR_UNSUPPORTED, "prefill: dtype %d not supported (bf16, fp16, fp32, fp8_e4m3fn)",
@@ -529,6 +537,8 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     p.kblock = (int32_t)(a->Sk > 0 ? a->Sk : 1);
     p.os_split = 0;
     p.lses_split = 0;
+    p.q_and = sp.q_and;
+    p.q_xor = sp.q_xor;
     const bool causal = a->causal != 0;
     if (a->dtype == DTATTN_FP32) {
         p.qk_ch = p.v_ch = (int32_t)(a->D / 4);

@@ -37,6 +37,8 @@ struct PrefillParams {
     // partial O and LSE at o + y os_split, lse + y lses_split; nsplit = 1 is the unsplit launch.
     int32_t nsplit, kblock;
     int64_t os_split, lses_split;
+    // q's words pass through (w & q_and) ^ q_xor at load: negation or zeroing for scales <= 0
+    uint32_t q_and, q_xor;
 };
 
 // Lazy rescaling: the running max only moves (and O, l are only rescaled) when some row's max grew

@@ -94,7 +94,7 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
         for (int ks = 0; ks < KSTEPS; ++ks) {
             u32x4 raw = {0u, 0u, 0u, 0u};
             if (qrow < p.Sq && (!PAD || (d0 >> 3) + 2 * ks + hf < p.qk_ch))
-                raw = ld16(qp + (int64_t)qrow * p.qs_s + d0 + ks * 16 + hf * 8);
+                raw = q_bits(ld16(qp + (int64_t)qrow * p.qs_s + d0 + ks * 16 + hf * 8), p.q_and, p.q_xor);
             qf[ks] = __builtin_bit_cast(V8, raw);
         }
     }

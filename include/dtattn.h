@@ -4,8 +4,8 @@
  * Every entry point takes device pointers, element strides and a HIP stream passed as `void*`
  * (a hipStream_t; NULL is the null stream).  Nothing here allocates device memory, creates or
  * switches streams, or synchronises: work is enqueued on `stream` and the call returns.  The
- * functions are reentrant; the only global state is a per-device property cache filled once under
- * std::call_once.  On failure they return a non-zero dtattn_status and dtattn_last_error() gives
+ * functions are reentrant; the only global state is a per-device property cache and the
+ * allocation-free decode's per-device scratch table, each filled once under std::call_once.  On failure they return a non-zero dtattn_status and dtattn_last_error() gives
  * a thread-local message (the C++ host op turns it into std::invalid_argument, the exception
  * SdpaOp's callers already handle: dtorch/core/kernel/kernel.cc:140-148).
  *
@@ -22,7 +22,12 @@
 extern "C" {
 #endif
 
-#define DTATTN_ABI_VERSION 7
+#define DTATTN_ABI_VERSION 8
+
+/* Softmax scale fields (ABI version 8): NaN selects 1/sqrt(D); any finite value is used as given,
+ * zero and negative included, as torch::scaled_dot_product_attention takes SdpaParam's scale
+ * (scaled_dot_product_attention_op.cc:107-109); +-inf is rejected.  Up to version 7 a scale <= 0
+ * selected 1/sqrt(D). */
 
 typedef enum {
     DTATTN_OK = 0,
@@ -72,7 +77,7 @@ typedef struct {
     int64_t lse_stride[2]; /* B, H (S stride is 1) */
     int32_t dtype;   /* dtattn_dtype of q, k, v */
     int32_t o_dtype; /* dtattn_dtype of o: equal to dtype, or BF16 / FP16 when dtype is FP8_E4M3FN */
-    float scale;     /* softmax scale; <= 0 means 1/sqrt(D) */
+    float scale;     /* softmax scale; NaN means 1/sqrt(D) (ABI version 8) */
     int32_t causal;
     int64_t q_offset, k_offset;
     const float* q_descale; /* FP8 only: [B, Hq] fp32, real = code * descale */
@@ -134,7 +139,7 @@ typedef struct {
     int64_t o_stride[2];   /* B, H */
     int64_t lse_stride[1]; /* B (H stride is 1) */
     int32_t dtype;         /* BF16, FP16 or FP32 (FP32 from ABI version 5) */
-    float scale;           /* <= 0 means 1/sqrt(D) */
+    float scale;           /* NaN means 1/sqrt(D) (ABI version 8) */
     int32_t chunk;         /* tokens per split: 128, 256, 384 or 512; 0 picks 128 when Hq / Hkv is a
                               multiple of 8 and Hkv is not, else 384 for bf16/fp16 and 256 for
                               fp32; workspace sizes for chunk 0 cover every choice */
@@ -186,7 +191,7 @@ typedef struct {
     int64_t lse_stride[1];     /* B (H stride is 1) */
     int64_t block_table_stride;/* elements between rows of block_table */
     int32_t dtype;             /* BF16, FP16 or FP32 (FP32 from ABI version 5) */
-    float scale;               /* <= 0 means 1/sqrt(D) */
+    float scale;               /* NaN means 1/sqrt(D) (ABI version 8) */
     int32_t chunk;             /* tokens per split: 128, 256, 384 or 512; 0 picks as dtattn_decode_args does */
     void* workspace;           /* >= dtattn_decode_paged_workspace_size(...) bytes, 256-byte aligned */
     size_t workspace_bytes;

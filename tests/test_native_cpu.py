@@ -84,6 +84,8 @@ def _last_error():
     (dict(dtype=2, o_dtype=0), 1, "descale"),
     (dict(q=0), 1, "null"),
     (dict(Sq=-1), 1, "bad sizes"),
+    (dict(scale=float("inf")), 1, "finite"),                         # NaN selects 1/sqrt(D); any finite scale runs
+    (dict(scale=float("-inf")), 1, "finite"),
 ])
 def test_prefill_validation(kw, code, text):
     lib.dtattn_prefill_fwd.restype = ctypes.c_int

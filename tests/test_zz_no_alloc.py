@@ -64,7 +64,7 @@ def _args(q, k, v, lengths, o, lse, code, chunk=0, ws=None):
     a.v_stride[:] = [v.stride(0), v.stride(1), v.stride(2)]
     a.o_stride[:] = [o.stride(0), o.stride(1)]
     a.lse_stride[:] = [lse.stride(0)]
-    a.dtype, a.scale, a.chunk = code, 0.0, chunk
+    a.dtype, a.scale, a.chunk = code, float("nan"), chunk  # NaN: 1/sqrt(D)
     a.workspace = ws.data_ptr() if ws is not None else None
     a.workspace_bytes = ws.numel() if ws is not None else 0
     return a
