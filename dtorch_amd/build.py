@@ -100,6 +100,17 @@ def build_host_extension() -> str:
     return out
 
 
+def build_c_client(src: str, out: str) -> str:
+    """A plain C program against include/dtattn.h and libdtattn.so (no torch): gcc with the HIP runtime's C
+    API, RPATH to the package directory and ROCm's libraries."""
+    rel = os.path.relpath(PKG, os.path.dirname(out))
+    _run(["gcc", "-O2", "-std=c11", "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{os.path.join(ROCM, 'include')}",
+          src, "-o", out + ".tmp", f"-L{PKG}", "-ldtattn", f"-L{os.path.join(ROCM, 'lib')}", "-lamdhip64", "-lm",
+          f"-Wl,-rpath,$ORIGIN/{rel}", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build() -> None:
     build_library()
     build_host_extension()

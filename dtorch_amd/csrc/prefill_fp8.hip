@@ -453,6 +453,9 @@ extern "C" int dtattn_prefill_fp8(const dtattn_prefill_args* a, void* stream_) {
     if (((reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->k) | reinterpret_cast<uintptr_t>(a->v) |
           reinterpret_cast<uintptr_t>(a->o)) & 15u) != 0)
         return fail(DTATTN_ERR_UNSUPPORTED, "prefill_fp8: tensors must be 16-byte aligned");
+    ScalePlan sp;
+    const int sst = plan_scale(a->scale, a->D, kSign16, &sp);  // q is rounded from its 16-bit rows
+    if (sst != DTATTN_OK) return sst;
     const Fp8Workspace w = fp8_workspace(a);
     if (a->workspace == nullptr || a->workspace_bytes < w.total || (reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
         return fail(DTATTN_ERR_WORKSPACE, "prefill_fp8: a 256-byte aligned workspace of %zu bytes is required, %zu given",
@@ -484,9 +487,6 @@ extern "C" int dtattn_prefill_fp8(const dtattn_prefill_args* a, void* stream_) {
     if (rc != DTATTN_OK) return rc;
 
     // 3. attention on the codes, Q rounded in the kernel
-    ScalePlan sp;
-    const int sst = plan_scale(a->scale, a->D, kSign16, &sp);  // q is rounded from its 16-bit rows
-    if (sst != DTATTN_OK) return sst;
     const float scale = sp.scale;
     int64_t delta64 = a->q_offset - a->k_offset;
     const int64_t lim = a->Sq + a->Sk + 1;
