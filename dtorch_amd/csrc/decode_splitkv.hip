@@ -43,6 +43,9 @@ struct DecodeParams {
     const int32_t* block_table;
     int64_t bt_s;
     int32_t page_shift, num_pages;
+    // bytes from a kv head's base to the end of its last page row (K, V), when every page offset fits 32 bits
+    // (strides >= 0, span < 2^32): the paged loads then go through buffer resources; 0: 64-bit flat loads
+    uint32_t kspan, vspan;
     // real head dim (<= the kernel's D; a multiple of 16 bytes of elements) and its 16-byte chunks
     int32_t d_real, d_ch;
     uint32_t q_and, q_xor;  // applied to q's words at load, as in ScalePlan
@@ -77,9 +80,11 @@ size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D_real, int
 
 // G heads per workgroup, D head dim, TPW tokens per wave (chunk = 4 * TPW, in sub-blocks per wave;
 // all trip counts are compile-time so each sub-block's loads issue together).
-// PAGED: rows are addressed through the block table with 64-bit loads of clamped token indices;
+// PAGED: 0, rows of a contiguous cache through a buffer resource over the chunk's rows; 1, rows of a paged
+// cache through the block table, with 64-bit loads of clamped token indices; 2, the same through a buffer
+// resource over the kv head's pages with 32-bit offsets, when they fit (DecodeParams::kspan);
 // otherwise through a buffer resource over the chunk's rows.
-template <typename T, int D, int G, int TPW, bool PAGED>
+template <typename T, int D, int G, int TPW, int PAGED>
 __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk: 8 (bf16, fp16) or 4 (fp32)
     constexpr int LPT = D / EPC;          // lanes per token row
@@ -166,10 +171,25 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
             }
             __builtin_amdgcn_sched_barrier(0);
             const int rmask = (1 << p.page_shift) - 1;
+            if constexpr (PAGED == 2) {
+                // 32-bit byte offsets into a resource over the head's pages: fewer address registers and
+                // instructions than 64-bit flat addresses (measured 4% faster on 16-token pages)
+                const auto kprs = make_rsrc(kp, p.kspan);
+                const auto vprs = make_rsrc(vp, p.vspan);
+                const uint32_t kpb = (uint32_t)(p.ks_b * sizeof(T)), kps = (uint32_t)(p.ks_s * sizeof(T));
+                const uint32_t vpb = (uint32_t)(p.vs_b * sizeof(T)), vps = (uint32_t)(p.vs_s * sizeof(T));
 #pragma unroll
-            for (int i = 0; i < NI; ++i) {  // the cache is read once per call
-                kr[i] = ld16_nt(kp + pg[i] * p.ks_b + (tr[i] & rmask) * p.ks_s + c8 * EPC);
-                vr[i] = ld16_nt(vp + pg[i] * p.vs_b + (tr[i] & rmask) * p.vs_s + c8 * EPC);
+                for (int i = 0; i < NI; ++i) {  // the cache is read once per call
+                    const uint32_t row = (uint32_t)(tr[i] & rmask);
+                    kr[i] = buf_ld16_nt(kprs, (uint32_t)pg[i] * kpb + row * kps + (uint32_t)c8 * 16u);
+                    vr[i] = buf_ld16_nt(vprs, (uint32_t)pg[i] * vpb + row * vps + (uint32_t)c8 * 16u);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {  // the cache is read once per call
+                    kr[i] = ld16_nt(kp + pg[i] * p.ks_b + (tr[i] & rmask) * p.ks_s + c8 * EPC);
+                    vr[i] = ld16_nt(vp + pg[i] * p.vs_b + (tr[i] & rmask) * p.vs_s + c8 * EPC);
+                }
             }
         } else {
 #pragma unroll
@@ -354,7 +374,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(const DecodeParams p)
     if (p.lse != nullptr && lane == 0) p.lse[b * p.lses_b + hq] = mx + __logf(sum);
 }
 
-template <typename T, int D, int G, int TPW, bool PAGED>
+template <typename T, int D, int G, int TPW, int PAGED>
 static int launch_decode(const DecodeParams& p, hipStream_t stream) {
     // Split index slowest: workgroups dispatched together read the same chunk of many sequences (and
     // the empty chunks of short sequences gather at the end of the grid).  Measured against split
@@ -368,7 +388,7 @@ static int launch_decode(const DecodeParams& p, hipStream_t stream) {
     return check_launch("decode_merge_kernel");
 }
 
-template <typename T, int D, int G, bool PAGED>
+template <typename T, int D, int G, int PAGED>
 static int dispatch_chunk(const DecodeParams& p, hipStream_t stream) {
     switch (p.chunk) {
         case 128: return launch_decode<T, D, G, 32, PAGED>(p, stream);
@@ -379,7 +399,7 @@ static int dispatch_chunk(const DecodeParams& p, hipStream_t stream) {
     }
 }
 
-template <typename T, int D, bool PAGED>
+template <typename T, int D, int PAGED>
 static int dispatch_group(const DecodeParams& p, hipStream_t stream) {
     const int g = p.group;
     // Groups of 8 heads: with Hkv a multiple of 8 the two 4-head subgroups of a kv head have workgroup
@@ -393,7 +413,7 @@ static int dispatch_group(const DecodeParams& p, hipStream_t stream) {
 }
 
 // D: the real head dim (a multiple of 16 bytes of elements, up to 128).
-template <typename T, bool PAGED>
+template <typename T, int PAGED>
 static int dispatch_decode(DecodeParams p, int D, hipStream_t stream) {
     const int Dk = decode_kernel_dim(D);
     if (Dk == 0 || (D * (int)sizeof(T)) % 16 != 0)
@@ -540,9 +560,10 @@ static int decode_splitkv_run(const dtattn_decode_args* a, void* ws, size_t ws_b
     p.bt_s = 0;
     p.page_shift = 0;
     p.num_pages = 0;
-    if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, false>(p, (int)a->D, stream);
-    if (a->dtype == DTATTN_FP32) return dispatch_decode<float, false>(p, (int)a->D, stream);
-    return dispatch_decode<f16_t, false>(p, (int)a->D, stream);
+    p.kspan = p.vspan = 0;
+    if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, 0>(p, (int)a->D, stream);
+    if (a->dtype == DTATTN_FP32) return dispatch_decode<float, 0>(p, (int)a->D, stream);
+    return dispatch_decode<f16_t, 0>(p, (int)a->D, stream);
 }
 
 }  // namespace dtattn
@@ -632,7 +653,21 @@ extern "C" int dtattn_decode_paged(const dtattn_decode_paged_args* a, void* stre
     p.bt_s = a->block_table_stride;
     p.page_shift = __builtin_ctzll((unsigned long long)a->page_size);
     p.num_pages = (int32_t)a->num_pages;
-    if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, true>(p, (int)a->D, stream);
-    if (a->dtype == DTATTN_FP32) return dispatch_decode<float, true>(p, (int)a->D, stream);
-    return dispatch_decode<f16_t, true>(p, (int)a->D, stream);
+    // byte span of one kv head's pages, for 32-bit buffer offsets when it fits
+    auto span = [&](const int64_t st[3]) -> uint32_t {
+        if (st[0] < 0 || st[2] < 0) return 0u;
+        const int64_t bytes = ((a->num_pages - 1) * st[0] + (a->page_size - 1) * st[2] + a->D) * esz;
+        return bytes < ((int64_t)1 << 32) ? (uint32_t)bytes : 0u;
+    };
+    p.kspan = span(a->k_stride);
+    p.vspan = span(a->v_stride);
+    if (p.kspan == 0 || p.vspan == 0) p.kspan = p.vspan = 0;
+    if (p.kspan != 0) {
+        if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, 2>(p, (int)a->D, stream);
+        if (a->dtype == DTATTN_FP32) return dispatch_decode<float, 2>(p, (int)a->D, stream);
+        return dispatch_decode<f16_t, 2>(p, (int)a->D, stream);
+    }
+    if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, 1>(p, (int)a->D, stream);
+    if (a->dtype == DTATTN_FP32) return dispatch_decode<float, 1>(p, (int)a->D, stream);
+    return dispatch_decode<f16_t, 1>(p, (int)a->D, stream);
 }

@@ -391,3 +391,40 @@ def test_decode_d64_default_splits(dtype, Hq, Hkv):
     co, cl = F.decode_attention(tq, _gather_dev(tk, bt, lengths, S), _gather_dev(tv, bt, lengths, S), tl, chunk=0)
     torch.cuda.synchronize()
     assert torch.equal(po, co) and torch.equal(pl, cl)
+
+
+def test_decode_paged_pool_past_4gb_takes_the_64bit_path():
+    # Page offsets of a kv head that do not fit 32 bits run the 64-bit flat loads; pools below that run
+    # 32-bit buffer offsets.  Both must give the bits of the contiguous kernel over the gathered cache.
+    # One 4.3 GB allocation holds K and V interleaved by page ([pages, 2, Hkv, ps, D]), so each pool's page
+    # stride is 16 KB and its span passes 4 GB; only the pages in the block table are written.
+    B, Hq, Hkv, ps, D = 2, 8, 2, 16, 128
+    num_pages = (1 << 32) // (2 * Hkv * ps * D * 2) + 2
+    pool = torch.empty(num_pages, 2, Hkv, ps, D, dtype=torch.bfloat16, device="cuda")
+    rng = np.random.default_rng(31)
+    lengths = np.array([300, 517], dtype=np.int32)
+    maxp = 33
+    used = np.concatenate([np.arange(3), rng.choice(np.arange(3, num_pages), size=2 * maxp - 3, replace=False)])
+    bt = used.reshape(B, maxp).astype(np.int32)
+    bt[1, -1] = num_pages - 1  # the last page of the pool, past 4 GB
+    vals = torch.randn(len(used), 2, Hkv, ps, D, device="cuda").to(torch.bfloat16)
+    pool[torch.from_numpy(bt.reshape(-1).astype(np.int64)).cuda()] = vals
+    kp, vp = pool[:, 0], pool[:, 1]
+    q = torch.randn(B, Hq, 1, D, device="cuda").to(torch.bfloat16)
+    tb, tl = torch.from_numpy(bt).cuda(), torch.from_numpy(lengths).cuda()
+    F = _F()
+    o, lse = F.decode_attention_paged(q, kp, vp, tb, tl, chunk=128)
+    # the contiguous kernel on the gathered rows, same split length
+    S = maxp * ps
+    kc = kp[tb.long()].permute(0, 2, 1, 3, 4).reshape(B, Hkv, S, D).contiguous()
+    vc = vp[tb.long()].permute(0, 2, 1, 3, 4).reshape(B, Hkv, S, D).contiguous()
+    o2, lse2 = F.decode_attention(q, kc, vc, tl, chunk=128)
+    # the same pages in a small pool: 32-bit offsets
+    small_k, small_v = kp[tb.long().reshape(-1)].contiguous(), vp[tb.long().reshape(-1)].contiguous()
+    tb_small = torch.arange(B * maxp, dtype=torch.int32, device="cuda").reshape(B, maxp)
+    o3, lse3 = F.decode_attention_paged(q, small_k, small_v, tb_small, tl, chunk=128)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert torch.equal(o3, o2) and torch.equal(lse3, lse2)
+    del pool, kp, vp
+    torch.cuda.empty_cache()
