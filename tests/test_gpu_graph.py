@@ -1,7 +1,9 @@
-"""The decode step under HIP graph capture: one KVCache.decode (append + split-KV decode + merge) captured,
+"""HIP graph capture.  The decode step: one KVCache.decode (append + split-KV decode + merge) captured,
 then replayed with new inputs.  Every replay must equal the eager step bit for bit: the kernels allocate
 nothing, clear nothing with memset, and read the sequence lengths from device memory, so a replay appends
-at the current length and advances it.  Eager work and synchronisations run between the replays.
+at the current length and advances it.  The prefill entry points (causal GQA, wide heads with key blocks and
+their merge, a mask, native fp8 in three launches, the ring step) captured the same way.  Eager work and
+synchronisations run between the replays.
 """
 import numpy as np
 import pytest
@@ -43,3 +45,40 @@ def test_decode_step_graph_replays_match_eager(dtype):
         assert torch.equal(out, ref[n]), j
         assert np.array_equal(cache.lengths.cpu().numpy(), np.full(B, j + 1))
     assert torch.equal(cache.k, eager.k) and torch.equal(cache.v, eager.v)
+
+
+@pytest.mark.parametrize("case", ["causal_gqa", "wide_key_blocks", "masked", "native_fp8", "ring_step"])
+def test_prefill_graph_replays_match_eager(case):
+    # The prefill entry points under capture, replayed with new inputs copied into the captured tensors:
+    # every replay equals the eager call bit for bit.  The wide-head case takes the key-block split, so its
+    # workspace and the LSE merge launch are captured too.
+    import dtorch_amd.nn.functional as F
+    rng = np.random.default_rng(sum(map(ord, case)))
+    shapes = {"causal_gqa": (2, 8, 2, 300, 300, 128), "wide_key_blocks": (1, 2, 1, 256, 2048, 512),
+              "masked": (1, 4, 4, 200, 260, 64), "native_fp8": (1, 4, 2, 256, 256, 128),
+              "ring_step": (1, 4, 2, 128, 256, 128)}  # a 128-row Q chunk against two 128-key chunks
+    B, Hq, Hkv, Sq, Sk, D = shapes[case]
+    mask = torch.from_numpy(rng.random((Sq, Sk)) < 0.7).cuda() if case == "masked" else None
+    opt = F.SdpaOption(sage_attn_type="native_fp8") if case == "native_fp8" else F.SdpaOption()
+
+    def call(q, k, v):
+        if case == "ring_step":
+            ks, vs = [k[:, :, :128], k[:, :, 128:]], [v[:, :, :128], v[:, :, 128:]]
+            return F.ring_attention_step(q, ks, vs, q_chunk_index=1)
+        return F.scaled_dot_product_attention_with_lse(q, k, v, is_causal=case in ("causal_gqa",), enable_gqa=True,
+                                                       attn_mask=mask, sdpa_option=opt)
+
+    inputs = [tuple(to_dev(randn(rng, (B, h, s, D))) for h, s in ((Hq, Sq), (Hkv, Sk), (Hkv, Sk))) for _ in range(3)]
+    ref = [tuple(t.clone() for t in call(*x)) for x in inputs]
+    torch.cuda.synchronize()
+    sq, sk, sv = (torch.zeros_like(t) for t in inputs[0])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = call(sq, sk, sv)
+    torch.cuda.synchronize()
+    for n in (0, 1, 2, 0):
+        for dst, src in zip((sq, sk, sv), inputs[n]):
+            dst.copy_(src)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(out, ref[n])), (case, n)
