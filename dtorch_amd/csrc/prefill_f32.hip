@@ -67,18 +67,8 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(const PrefillParams
     }
     const int nt = (kend + BN - 1) / BN;
 
-    // Q fragment (B operand of S^T = K Q^T): lane (l32, hf) holds Q[wq0 + l32][HD*hf + s], s < HD.
+    // Q fragment (B operand of S^T = K Q^T), loaded after the first tile's loads are issued
     float qf[HD];
-    {
-        const int qrow = wq0 + l32;
-#pragma unroll
-        for (int g = 0; g < HD / 4; ++g) {
-            u32x4 raw = {0u, 0u, 0u, 0u};
-            if (qrow < p.Sq) raw = q_bits(ld16(qp + (int64_t)qrow * p.qs_s + HD * hf + 4 * g), p.q_and, p.q_xor);
-            const f32x4 x = __builtin_bit_cast(f32x4, raw);
-            qf[4 * g + 0] = x.x, qf[4 * g + 1] = x.y, qf[4 * g + 2] = x.z, qf[4 * g + 3] = x.w;
-        }
-    }
 
     f32x16 oacc[DT];
 #pragma unroll
@@ -231,6 +221,20 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(const PrefillParams
     if (nt > 0) {
         dma(Ka, kp, krow, p.ks_s, 0);
         dma(Va, vp, vrow, p.vs_s, 0);
+    }
+    // Lane (l32, hf) holds Q[wq0 + l32][HD*hf + s], s < HD.  Unconditional loads issue back to back and
+    // share the first tile's memory latency (a branch per load serialised them); rows past Sq read row
+    // Sq-1 and are zeroed by the mask.
+    {
+        const int qrow = wq0 + l32;
+        const bool row_ok = qrow < p.Sq;
+        const float* qsrc = qp + (int64_t)(row_ok ? qrow : p.Sq - 1) * p.qs_s + HD * hf;
+#pragma unroll
+        for (int g = 0; g < HD / 4; ++g) {
+            const u32x4 raw = q_bits(ld16(qsrc + 4 * g), row_ok ? p.q_and : 0u, row_ok ? p.q_xor : 0u);
+            const f32x4 x = __builtin_bit_cast(f32x4, raw);
+            qf[4 * g + 0] = x.x, qf[4 * g + 1] = x.y, qf[4 * g + 2] = x.z, qf[4 * g + 3] = x.w;
+        }
     }
     // Q fragments (and tile 0) complete here, visibly to the compiler, so that it inserts no load
     // waits inside the loop (where they would also drain the asynchronous tile loads).

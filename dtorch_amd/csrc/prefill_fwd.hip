@@ -91,18 +91,7 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     }
     const int nt = (kend + BN - 1) / BN;
 
-    // Q fragments (B operand of S^T = K Q^T): lane holds query l32, d = ks*16 + hf*8 .. +8.
-    V8 qf[KSTEPS];
-    {
-        const int qrow = wq0 + l32;
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-            u32x4 raw = {0u, 0u, 0u, 0u};
-            if (qrow < p.Sq && (!PAD || 2 * ks + hf < p.qk_ch))
-                raw = q_bits(ld16(qp + (int64_t)qrow * p.qs_s + ks * 16 + hf * 8), p.q_and, p.q_xor);
-            qf[ks] = __builtin_bit_cast(V8, raw);
-        }
-    }
+    V8 qf[KSTEPS];  // Q fragments (B operand of S^T = K Q^T), loaded after tile 0's loads are issued
 
     f32x16 oacc[DT];
 #pragma unroll
@@ -302,6 +291,22 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
     if (nt > 0) {
         dma(Ka, kp, krow, p.ks_s, 0, p.qk_ch);
         dma(Va, vp, vrow, p.vs_s, 0, p.v_ch);
+    }
+    // Q fragments: lane holds query l32, d = ks*16 + hf*8 .. +8.  Issued after tile 0's loads so that
+    // the two share one memory latency.  The loads are unconditional, so they issue back to back (a
+    // branch per load made the compiler wait for each in turn: 8 round trips, ~3.7 us of a C2
+    // workgroup's start).  Rows past Sq read row Sq-1 and chunks past qk_ch read chunk 0; the mask
+    // zeroes both.
+    {
+        const int qrow = wq0 + l32;
+        const bool row_ok = qrow < p.Sq;
+        const T* qsrc = qp + (int64_t)(row_ok ? qrow : p.Sq - 1) * p.qs_s;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            const bool ok = row_ok && (!PAD || 2 * ks + hf < p.qk_ch);
+            const u32x4 w = ld16(qsrc + (ok ? ks * 16 + hf * 8 : 0));
+            qf[ks] = __builtin_bit_cast(V8, q_bits(w, ok ? p.q_and : 0u, ok ? p.q_xor : 0u));
+        }
     }
     // Q fragments (and tile 0) complete here, visibly to the compiler, so that it inserts no load
     // waits inside the loop (where they would also drain the asynchronous tile loads).

@@ -86,18 +86,8 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
     const int t0 = kb0 / BN;
     const int nt = kend > kb0 ? (kend + BN - 1) / BN : t0;
 
-    // Q fragment of the wave's half (B operand of S^T): lane holds query l32, d = d0 + ks*16 + hf*8 .. +8.
+    // Q fragment of the wave's half (B operand of S^T), loaded after the first tile's loads are issued
     V8 qf[KSTEPS];
-    {
-        const int qrow = wq0 + l32;
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-            u32x4 raw = {0u, 0u, 0u, 0u};
-            if (qrow < p.Sq && (!PAD || (d0 >> 3) + 2 * ks + hf < p.qk_ch))
-                raw = q_bits(ld16(qp + (int64_t)qrow * p.qs_s + d0 + ks * 16 + hf * 8), p.q_and, p.q_xor);
-            qf[ks] = __builtin_bit_cast(V8, raw);
-        }
-    }
     f32x16 oacc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -272,6 +262,20 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
     if (nt > t0) {
         dma(Ka, kp, krow, p.ks_s, t0, p.qk_ch);
         dma(Va, vp, vrow, p.vs_s, t0, p.v_ch);
+    }
+    // Lane holds query l32, d = d0 + ks*16 + hf*8 .. +8.  Unconditional loads issue back to back and share
+    // the first tile's memory latency (a branch per load serialised them).  Rows past Sq read row Sq-1 and
+    // chunks past qk_ch read the half's first chunk; the mask zeroes both.
+    {
+        const int qrow = wq0 + l32;
+        const bool row_ok = qrow < p.Sq;
+        const T* qsrc = qp + (int64_t)(row_ok ? qrow : p.Sq - 1) * p.qs_s + d0;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            const bool ok = row_ok && (!PAD || (d0 >> 3) + 2 * ks + hf < p.qk_ch);
+            const u32x4 w = ld16(qsrc + (ok ? ks * 16 + hf * 8 : 0));
+            qf[ks] = __builtin_bit_cast(V8, q_bits(w, ok ? p.q_and : 0u, ok ? p.q_xor : 0u));
+        }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): Q and the first tile, visibly to the compiler
     for (int t = t0; t < nt; t += 2) {
