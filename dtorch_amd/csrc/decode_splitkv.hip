@@ -84,6 +84,10 @@ size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D_real, int
 // cache through the block table, with 64-bit loads of clamped token indices; 2, the same through a buffer
 // resource over the kv head's pages with 32-bit offsets, when they fit (DecodeParams::kspan);
 // otherwise through a buffer resource over the chunk's rows.
+// The sub-block loop of one fp32 instantiation (three 32-token sub-blocks per wave) is too large to
+// unroll fully and stays a loop; each iteration still issues its sub-block's loads together.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wpass-failed"
 template <typename T, int D, int G, int TPW, int PAGED>
 __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk: 8 (bf16, fp16) or 4 (fp32)
@@ -323,6 +327,8 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
         }
     }
 }
+
+#pragma clang diagnostic pop
 
 // One wave per (b, query head): merge the ceil(L_b / C) partials by LSE (sequences that fit in one
 // chunk were written directly by decode_kernel).
