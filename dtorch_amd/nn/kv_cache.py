@@ -32,10 +32,23 @@ class KVCache:
         self.lengths = torch.zeros(batch, dtype=torch.int32, device=device)
         self.scale = scale
         self._host_len = np.zeros(batch, dtype=np.int64)  # mirrors `lengths` for capacity checks
+        self._host_stale = False  # a step was recorded under graph capture: replays outrun _host_len
 
     @property
     def capacity(self) -> int:
         return self.k.shape[2]
+
+    def _span(self) -> int:
+        """Cache positions the decode kernel covers.  Its split grid is sized by S_max, so in eager use the
+        cache is passed as a view up to the longest sequence rather than the whole capacity (one split per
+        384 tokens of S_max, empty ones included: a 32K-token cache holding 2K-token sequences would launch
+        16x the workgroups).  Under graph capture, and after it until sync_lengths(), the host does not
+        know the lengths the replays reach, so the whole capacity is covered."""
+        if torch.cuda.is_current_stream_capturing():
+            self._host_stale = True
+        if self._host_stale:
+            return self.capacity
+        return max(int(self._host_len.max(initial=0)), 1)
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
         """Append [B, Hkv, n, D] keys and values after each sequence's current length."""
@@ -57,7 +70,8 @@ class KVCache:
     def decode(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> torch.Tensor:
         """One new token per sequence: append its K/V, then attend over everything cached."""
         self.append(k_new, v_new)
-        return F.decode_attention(q, self.k, self.v, self.lengths, scale=self.scale)[0]
+        n = self._span()
+        return F.decode_attention(q, self.k[:, :, :n], self.v[:, :, :n], self.lengths, scale=self.scale)[0]
 
     def sync_lengths(self) -> np.ndarray:
         """Refresh the host copy of the lengths from the device (one synchronising copy).
@@ -69,6 +83,7 @@ class KVCache:
         saturate there), so later replays would attend over a truncated cache.
         """
         self._host_len = self.lengths.to("cpu", torch.int64).numpy().copy()
+        self._host_stale = False
         return self._host_len.copy()
 
 
@@ -91,6 +106,17 @@ class PagedKVCache:
         self._host_len = np.zeros(batch, dtype=np.int64)
         self.block_table = torch.from_numpy(self._table).to(device)
         self.lengths = torch.zeros(batch, dtype=torch.int32, device=device)
+        self._host_stale = False  # a step was recorded under graph capture: replays outrun _host_len
+
+    def _span_pages(self) -> int:
+        """Block-table columns the decode kernel covers: the most pages any sequence holds in eager use
+        (the split grid is sized by max_pages * page_size), the whole table under graph capture and after
+        it until sync_lengths()."""
+        if torch.cuda.is_current_stream_capturing():
+            self._host_stale = True
+        if self._host_stale:
+            return self._table.shape[1]
+        return max(int(self._pages.max(initial=0)), 1)
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
         n = k_new.shape[2]
@@ -119,7 +145,8 @@ class PagedKVCache:
 
     def decode(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> torch.Tensor:
         self.append(k_new, v_new)
-        return F.decode_attention_paged(q, self.k, self.v, self.block_table, self.lengths, scale=self.scale)[0]
+        n = self._span_pages()
+        return F.decode_attention_paged(q, self.k, self.v, self.block_table[:, :n], self.lengths, scale=self.scale)[0]
 
     def sync_lengths(self) -> np.ndarray:
         """Refresh the host copy of the lengths from the device after HIP-graph replays.
@@ -132,4 +159,5 @@ class PagedKVCache:
         if np.any(dev > self._pages * self.page_size):
             raise RuntimeError("PagedKVCache: graph replays appended past the assigned pages")
         self._host_len = dev
+        self._host_stale = False
         return dev.copy()

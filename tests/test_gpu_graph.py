@@ -45,6 +45,11 @@ def test_decode_step_graph_replays_match_eager(dtype):
         assert torch.equal(out, ref[n]), j
         assert np.array_equal(cache.lengths.cpu().numpy(), np.full(B, j + 1))
     assert torch.equal(cache.k, eager.k) and torch.equal(cache.v, eager.v)
+    # the replays advanced the device lengths past the host copy: eager decode keeps covering the whole
+    # capacity until sync_lengths() refreshes it
+    assert cache._span() == cache.capacity
+    assert np.array_equal(cache.sync_lengths(), np.full(B, T))
+    assert cache._span() == T
 
 
 @pytest.mark.parametrize("case", ["causal_gqa", "wide_key_blocks", "masked", "native_fp8", "ring_step"])

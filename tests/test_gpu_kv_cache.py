@@ -85,6 +85,34 @@ def test_decode_loop_equals_causal_attention(paged):
     assert np.array_equal(cache.lengths.cpu().numpy(), np.full(B, T))
 
 
+@pytest.mark.parametrize("paged", [False, True])
+def test_decode_covers_the_longest_sequence_not_the_capacity(paged):
+    # A cache far larger than its sequences: decode runs over a view up to the longest one (the split grid
+    # follows S_max), and must equal the call over the whole cache bit for bit.
+    from dtorch_amd.nn.kv_cache import KVCache, PagedKVCache
+    F = _F()
+    rng = np.random.default_rng(44 + paged)
+    B, Hq, Hkv, D, L0 = 3, 8, 2, 128, 700
+    q, k, v = randn(rng, (B, Hq, L0 + 3, D)), randn(rng, (B, Hkv, L0 + 3, D)), randn(rng, (B, Hkv, L0 + 3, D))
+    tq, tk, tv = to_dev(q), to_dev(k), to_dev(v)
+    if paged:
+        cache = PagedKVCache(B, Hkv, num_pages=B * 200, page_size=16, max_pages=200, head_dim=D)
+    else:
+        cache = KVCache(B, Hkv, max_len=16384, head_dim=D)
+    cache.prefill(tq[:, :, :L0], tk[:, :, :L0], tv[:, :, :L0])
+    for j in range(L0, L0 + 3):
+        s = slice(j, j + 1)
+        o = cache.decode(tq[:, :, s], tk[:, :, s], tv[:, :, s])
+        if paged:
+            assert cache._span_pages() == (j + 1 + 15) // 16 < 200
+            full = F.decode_attention_paged(tq[:, :, s], cache.k, cache.v, cache.block_table, cache.lengths)[0]
+        else:
+            assert cache._span() == j + 1 < cache.capacity
+            full = F.decode_attention(tq[:, :, s], cache.k, cache.v, cache.lengths)[0]
+        torch.cuda.synchronize()
+        assert torch.equal(o, full), j
+
+
 def test_kv_cache_capacity_is_checked_on_the_host():
     from dtorch_amd.nn.kv_cache import KVCache, PagedKVCache
     cache = KVCache(1, 1, max_len=4, head_dim=64)
