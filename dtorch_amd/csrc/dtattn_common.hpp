@@ -171,13 +171,19 @@ __device__ __forceinline__ u32x4 buf_ld16_nt(__amdgpu_buffer_rsrc_t r, uint32_t 
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 2));
 }
 
-// 16 bytes per lane straight into LDS (lane l lands at lds + 16 * l; lds is wave-uniform), issued from
-// inline assembly so the compiler's wait-count pass does not track it (it cannot always prove that later
-// reads of other LDS buffers do not alias the copy and would drain it with vmcnt(0)).  The caller owns
-// completion: an explicit wait_vmem() plus a barrier before any wave reads the destination.
+// 16 bytes per lane straight into LDS (lane l lands at lds + 16 * l; lds is wave-uniform).  The compiler
+// tracks this form in its wait counts, and its scheduler can place the load between MFMAs.
+__device__ __forceinline__ void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+}
+
+// The same load issued from inline assembly, so the compiler's wait-count pass does not track it (it
+// cannot always prove that later reads of other LDS buffers do not alias the copy and would drain it with
+// vmcnt(0)).  The caller owns completion: an explicit wait_vmem() plus a barrier before any wave reads the
+// destination.
 // m0 carries the LDS address.  The compiler reserves m0 and warns that it may not honour the clobber
-// (-Winline-asm, silenced here); the kernels' generated code holds no value of its own in m0 (this is the
-// only instruction that sets it, and the builtin form of the load, which also sets m0, is not used).
+// (-Winline-asm, silenced here).  No kernel holds a value of its own in m0, and none uses both forms (the
+// builtin form sets m0 as well).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void buf_ld16_lds_async(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {

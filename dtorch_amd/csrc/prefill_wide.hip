@@ -118,6 +118,34 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
         }
     };
 
+    constexpr int DMA_ROWS = 1024 / (2 * D);             // rows per load instruction
+    constexpr int DMA_INSTR = BN / DMA_ROWS / NW;  // per wave, per tensor and tile
+    static_assert(DMA_INSTR >= 1, "at least one load per wave");
+    // At D = 512 (one wave per SIMD) tile t+1's loads are spread over tile t's MFMAs: K's between the S
+    // MFMAs, V's after the PV block.  Issued in one burst at the tile start, a wave's 16 one-row loads
+    // stalled its issue for ~1,700 cycles while the memory pipeline took them, with no other wave on the
+    // SIMD.  That form uses the compiler-tracked load, which the scheduler can place between MFMAs.  The
+    // D = 256 kernels keep the untracked burst, and so do the masked ones: their mask loads are tracked too,
+    // and since the memory counter retires in order, each wait for a mask value would also wait for the
+    // tile loads issued before it (5 to 33 waits per tile in the generated code).  Causal D = 512 kernels
+    // keep it as well: the spread form measured 28-31% slower there (1x8x2048, D = 512 and 320).
+    constexpr bool kSpreadDma = D >= 512 && !MASKED && !CAUSAL;
+    // Resource over tile t's valid rows.  Past the last tile it covers nothing: every load is then out of
+    // range and lands zeros in a buffer no wave reads again.
+    auto dma_rs = [&](const T* base, int pitch, int64_t stride, int t, int valid_ch, uint32_t* nb) {
+        const int rows = min(BN, p.Sk - t * BN);
+        *nb = rows > 0 ? (uint32_t)((rows - 1) * pitch + (PAD ? valid_ch * 16 : D * (int)sizeof(T))) : 0u;
+        return make_rsrc(base + (rows > 0 ? (int64_t)t * BN * stride : 0), *nb);
+    };
+    // Load i of this wave's share of a tile, in the tracked form.
+    auto dma_one = [&](T* dst, __amdgpu_buffer_rsrc_t rs, uint32_t nbytes, int pitch, int valid_ch, int i) {
+        const int r0 = (wave * DMA_INSTR + i) * DMA_ROWS;
+        const int r = r0 + lane / DCH;
+        const int c = (lane % DCH) ^ wswz(r);
+        const uint32_t off = (PAD && c >= valid_ch) ? nbytes : (uint32_t)(r * pitch + c * 16);
+        buf_ld16_lds(rs, dst + r0 * D, off);
+    };
+
     // V^T reads (ds_read_b64_tr_b16), as in the main kernel: within each 16-lane block, lane 4j+a
     // addresses key K0+j, d-segment D0+4a.
     const int blk = lane >> 4, bl = lane & 15;
@@ -136,9 +164,14 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
     auto tile = [&](const T* Kc, const T* Vc, T* Kn, T* Vn, int t) {
         wait_vmem();
         lds_barrier();  // tile t landed; every wave finished tile t-1, including its exchange reads
-        if (t + 1 < nt) {
-            dma(Kn, kp, krow, p.ks_s, t + 1, p.qk_ch);
-            dma(Vn, vp, vrow, p.vs_s, t + 1, p.v_ch);
+        uint32_t knb = 0, vnb = 0;
+        const auto krs_n = dma_rs(kp, krow, p.ks_s, t + 1, p.qk_ch, &knb);
+        const auto vrs_n = dma_rs(vp, vrow, p.vs_s, t + 1, p.v_ch, &vnb);
+        if constexpr (!kSpreadDma) {
+            if (t + 1 < nt) {
+                dma(Kn, kp, krow, p.ks_s, t + 1, p.qk_ch);
+                dma(Vn, vp, vrow, p.vs_s, t + 1, p.v_ch);
+            }
         }
         const int kbase = t * BN;
         // Every row of this row group precedes the tile: the pair skips it together (both waves still
@@ -154,7 +187,12 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
         f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.f;
-        if (!skip) {
+        if (skip) {
+            if constexpr (kSpreadDma) {
+#pragma unroll
+                for (int i = 0; i < DMA_INSTR; ++i) dma_one(Kn, krs_n, knb, krow, p.qk_ch, i);
+            }
+        } else {
 #pragma unroll
             for (int ks = 0; ks < KSTEPS; ++ks) {
                 const int r = l32;
@@ -164,20 +202,40 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
             }
             // K fragment reads run four MFMAs ahead of their use: at D = 512 the wave runs alone on its
             // SIMD, so an LDS read that has not returned stalls the matrix pipe (two ahead: 8% slower)
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            if constexpr (kSpreadDma) {
+                // tile t+1's K loads, one after every KSTEPS / DMA_INSTR MFMAs
 #pragma unroll
-            for (int i = 0; i < KSTEPS - 4; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                for (int i = 0; i < DMA_INSTR; ++i) dma_one(Kn, krs_n, knb, krow, p.qk_ch, i);
+                constexpr int EVERY = KSTEPS / DMA_INSTR;
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+                for (int i = 0; i < KSTEPS; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (i < KSTEPS - 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if (i % EVERY == EVERY - 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+                for (int i = 0; i < KSTEPS - 4; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 *reinterpret_cast<f32x4*>(sx_mine + 4 * (j ^ sxs)) =
                     f32x4{s[4 * j], s[4 * j + 1], s[4 * j + 2], s[4 * j + 3]};
         }
         lds_barrier();  // every partial written
-        if (skip) return;
+        if (skip) {
+            if constexpr (kSpreadDma) {
+#pragma unroll
+                for (int i = 0; i < DMA_INSTR; ++i) dma_one(Vn, vrs_n, vnb, vrow, p.v_ch, i);
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const f32x4 x = *reinterpret_cast<const f32x4*>(sx_partner + 4 * (j ^ sxs));
@@ -247,6 +305,10 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
                 oacc[dt] = Elem<T>::mfma32(a, pb[ks], oacc[dt]);
             }
         }
+        if constexpr (kSpreadDma) {  // tile t+1's V loads (they stay after the V^T reads of this buffer's twin)
+#pragma unroll
+            for (int i = 0; i < DMA_INSTR; ++i) dma_one(Vn, vrs_n, vnb, vrow, p.v_ch, i);
+        }
         // V^T reads (two per MFMA) run two MFMAs ahead (one ahead: 8% slower at D = 512, 6-9% at D = 256;
         // three ahead: no faster).  Spreading the exponentials of P chunk 1 over these MFMAs measured
         // 4-7% slower than computing P first.
@@ -260,8 +322,18 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
     };
 
     if (nt > t0) {
-        dma(Ka, kp, krow, p.ks_s, t0, p.qk_ch);
-        dma(Va, vp, vrow, p.vs_s, t0, p.v_ch);
+        if constexpr (kSpreadDma) {  // one form of the load per kernel: the tracked one sets m0 itself
+            uint32_t kb0 = 0, vb0 = 0;
+            const auto krs0 = dma_rs(kp, krow, p.ks_s, t0, p.qk_ch, &kb0);
+            const auto vrs0 = dma_rs(vp, vrow, p.vs_s, t0, p.v_ch, &vb0);
+#pragma unroll
+            for (int i = 0; i < DMA_INSTR; ++i) dma_one(Ka, krs0, kb0, krow, p.qk_ch, i);
+#pragma unroll
+            for (int i = 0; i < DMA_INSTR; ++i) dma_one(Va, vrs0, vb0, vrow, p.v_ch, i);
+        } else {
+            dma(Ka, kp, krow, p.ks_s, t0, p.qk_ch);
+            dma(Va, vp, vrow, p.vs_s, t0, p.v_ch);
+        }
     }
     // Lane holds query l32, d = d0 + ks*16 + hf*8 .. +8.  Unconditional loads issue back to back and share
     // the first tile's memory latency (a branch per load serialised them).  Rows past Sq read row Sq-1 and
