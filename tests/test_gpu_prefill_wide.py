@@ -78,6 +78,8 @@ def test_vae_attention_16k_pixels_sampled_rows():
     (1, 4, 1, 700, 1500, 256, True, 800, torch.float16),    # GQA 4, causal with a query offset
     (1, 1, 1, 333, 2000, 320, False, 0, torch.bfloat16),    # padded head dim in key blocks
     (2, 4, 4, 2048, 2048, 512, False, 0, torch.bfloat16),   # a full grid: no split
+    (1, 2, 1, 500, 1001, 512, False, 0, torch.float16),     # fp16, GQA 2, a ragged tail in the last block
+    (2, 8, 4, 1000, 1001, 512, False, 0, torch.bfloat16),   # a full grid, ragged keys and queries
 ])
 def test_prefill_wide_key_blocks(B, Hq, Hkv, Sq, Sk, D, causal, q_offset, dtype):
     # Grids smaller than the CU count run the keys as several blocks merged by LSE; every row and the LSE
