@@ -69,7 +69,9 @@ class Timer:
     def __init__(self, torch):
         self.torch = torch
 
-    def run(self, fn, reps, settle=0.15, flush=None):
+    def run(self, fn, reps, settle=0.15, flush=None, batch=1):
+        """Median and mean seconds per call over `reps` timed groups of `batch` back-to-back calls (the host
+        runs ahead of the GPU inside a group, so a call's Python and launch overhead is not GPU idle time)."""
         t = self.torch
         t0 = time.perf_counter()
         n = 0
@@ -85,10 +87,11 @@ class Timer:
                 flush()
             s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
             s.record()
-            fn()
+            for _ in range(batch):
+                fn()
             e.record()
             e.synchronize()
-            times.append(s.elapsed_time(e) * 1e-3)
+            times.append(s.elapsed_time(e) * 1e-3 / batch)
         return float(np.median(times)), float(np.mean(times))
 
 
@@ -288,16 +291,18 @@ def secondary_workloads(torch, F, dev, timer, cpu_info=None, cpu_seconds=0.0):
     # MMDiT joint attention, bf16 and fp8
     q5, k5, v5 = (torch.randn(1, 24, 4608, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
     f5 = 4 * 24 * 128 * 4608 * 4608
-    med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5), reps=10)
+    med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5), reps=10, batch=4)
     extras["mmdit_c5a_bf16"] = {"TFLOP/s": round(f5 / med / 1e12, 1), "frac_bf16": round(f5 / med / PEAK_BF16, 4),
                                 "us": round(med * 1e6, 1)}
     # fp8: the native_fp8 op end to end (per-head quantization of q, k, v plus the attention, three
-    # launches), and the attention kernel alone on codes quantized beforehand (the codes entry point)
+    # launches and the tail merge), and the attention alone on codes quantized beforehand (the codes entry
+    # point: the attention kernel and the tail merge)
     from dtorch_amd import _lib
     opt = F.SdpaOption(sage_attn_type="native_fp8")
-    med8, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5, sdpa_option=opt), reps=10)
+    med8, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5, sdpa_option=opt), reps=10,
+                        batch=4)
     (q8, qd), (k8, kd), (v8, vd) = (F.quantize_fp8_per_head(x) for x in (q5, k5, v5))
-    kern8, _ = timer.run(lambda: _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, torch.bfloat16), reps=10)
+    kern8, _ = timer.run(lambda: _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, torch.bfloat16), reps=10, batch=4)
     extras["mmdit_c5b_fp8"] = {"TFLOP/s_end_to_end": round(f5 / med8 / 1e12, 1),
                                "TFLOP/s_attention_kernel": round(f5 / kern8 / 1e12, 1),
                                "frac_fp8_kernel": round(f5 / kern8 / PEAK_FP8, 4),

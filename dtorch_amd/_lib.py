@@ -86,10 +86,13 @@ class DecodeArgs(ctypes.Structure):
             self.scale = float("nan")
 
 
-def prefill_fp8_codes(q8, k8, v8, qd, kd, vd, out_dtype, causal=False, q_offset=0, k_offset=0, scale=None):
+def prefill_fp8_codes(q8, k8, v8, qd, kd, vd, out_dtype, causal=False, q_offset=0, k_offset=0, scale=None,
+                      split=True):
     """Attention on e4m3fn codes with per-head descales (dtattn_prefill_fwd, dtype FP8_E4M3FN): the kernel of
     the native fp8 path on codes the caller quantized already.  q8/k8/v8 are contiguous float8_e4m3fn
-    [B, H, S, D] device tensors, qd/kd/vd fp32 [B, H]; returns (O [B, Hq, Sq, D] in out_dtype, LSE fp32)."""
+    [B, H, S, D] device tensors, qd/kd/vd fp32 [B, H]; returns (O [B, Hq, Sq, D] in out_dtype, LSE fp32).
+    With `split` the call gets the workspace dtattn_prefill_workspace_size() asks for (the tail split of
+    non-causal grids, as the native path runs it); without, it runs unsplit."""
     import torch
     B, Hq, Sq, D = q8.shape
     Hkv, Sk = k8.shape[1], k8.shape[2]
@@ -106,6 +109,15 @@ def prefill_fp8_codes(q8, k8, v8, qd, kd, vd, out_dtype, causal=False, q_offset=
     a.causal, a.q_offset, a.k_offset = int(causal), int(q_offset), int(k_offset)
     a.q_descale, a.k_descale, a.v_descale = qd.data_ptr(), kd.data_ptr(), vd.data_ptr()
     lib = cabi()
+    ws = None
+    if split:
+        lib.dtattn_prefill_workspace_size.argtypes = [ctypes.c_void_p]
+        lib.dtattn_prefill_workspace_size.restype = ctypes.c_size_t
+        with torch.cuda.device(q8.device):
+            nbytes = lib.dtattn_prefill_workspace_size(ctypes.byref(a))
+        if nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=q8.device)  # the caching allocator aligns to 512 B
+            a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
     lib.dtattn_prefill_fwd.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     lib.dtattn_last_error.restype = ctypes.c_char_p
     st = lib.dtattn_prefill_fwd(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(q8.device).cuda_stream))

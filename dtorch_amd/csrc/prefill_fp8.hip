@@ -24,6 +24,8 @@
 //   sum l accumulated over the same 2^7-scaled P.
 #include <string.h>
 
+#include <atomic>
+
 #include "dtattn_common.hpp"
 #include "fp8_quant.hpp"
 
@@ -50,7 +52,33 @@ struct PrefillFp8Params {
     float c;
     int32_t xcd_map;
     uint32_t q_and, q_xor;  // applied to q's words at load (codes or 16-bit rows), as in ScalePlan
+    // Tail split (non-causal only): workgroups below n_full take whole query blocks; the query blocks
+    // n_full .. of the plain grid run as tail_s pieces of tail_tiles key tiles each, which store their
+    // partials in tail_part for fp8_tail_merge_kernel.
+    int32_t n_full, tail_s, tail_tiles;
+    uint8_t* tail_part;
 };
+
+// Bytes of one tail piece's partial: its O normalised by its own row sum, in fp16 (an average of V codes,
+// so within +-448), as [wave][pair of 4-value groups][lane][8] in the accumulator's register order; then
+// the running max and the row sum in fp32 as [wave][lane][2].
+template <int D>
+constexpr int64_t fp8_tail_o_bytes() { return 4 * (D / 32) * 2 * 64 * 16; }
+template <int D>
+constexpr int64_t fp8_tail_part_bytes() { return fp8_tail_o_bytes<D>() + 4 * 64 * 8; }
+constexpr int kFp8TailMaxPieces = 8;
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats as fp16 (round to nearest even) in one word, and back.
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, f16x2{(_Float16)a, (_Float16)b});
+}
+__device__ __forceinline__ f32x2 unpack_f16x2(uint32_t w) {
+    const f16x2 h = __builtin_bit_cast(f16x2, w);
+    return f32x2{(float)h[0], (float)h[1]};
+}
 
 // P enters the PV MFMA as e4m3 codes of P * 2^kPScaleLog2.  With lazy rescaling P can exceed 1 by up
 // to 2^kFp8RescaleThreshold before the running max moves, so 2^(7 + 1.5) = 362 stays below the e4m3
@@ -64,6 +92,49 @@ constexpr float kFp8RescaleThreshold = 1.5f;
 template <int D>
 __device__ __forceinline__ int fswz(int r) {
     return D >= 128 ? (2 * ((r >> 1) & 3)) ^ ((r >> 5) & 1) : (2 * ((r >> 2) & 1)) ^ ((r >> 5) & 1);
+}
+
+// Normalises one wave's 32 query rows and writes them: O^T accumulators `oacc` (lane: row l32, d rows of
+// half hf), running max `mrow` (log2 units) and row sum `l`, both of the 2^kPScaleLog2-scaled P.  O is staged through the wave's slab `Os` of 32 x D 16-bit values in LDS
+// (16-byte chunk c of row r at c ^ (r % (D / 8))) for 16-byte coalesced row stores.  Holds workgroup
+// barriers: every wave of the workgroup calls it.
+template <int D, typename TO>
+__device__ __forceinline__ void fp8_write_rows(const PrefillFp8Params& p, int b, int hq, int wq0, const f32x16* oacc,
+                                               float mrow, float l, float vdesc, TO* Os) {
+    typedef typename Elem<TO>::vec4 O4;
+    constexpr int OCH = D / 8;  // 16-byte chunks per 16-bit output row
+    constexpr int DT = D / 32;
+    const int lane = threadIdx.x & 63, hf = lane >> 5;
+    {
+        const float inv = l > 0.f ? vdesc / l : 0.f;
+        const int row = lane & 31;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                O4 o4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o4[e] = Elem<TO>::from_f32(oacc[dt][4 * i4 + e] * inv);
+                const int c = dt * 4 + i4;
+                *reinterpret_cast<O4*>(Os + row * D + 8 * (c ^ (row % OCH)) + 4 * hf) = o4;
+            }
+        if (p.lse != nullptr && hf == 0) {
+            const int qrow = wq0 + row;
+            if (qrow < p.Sq) {
+                const float lse = l > 0.f ? (mrow + __log2f(l) - kPScaleLog2) * kLn2 : kNegInf;
+                p.lse[b * p.lses_b + hq * p.lses_h + qrow] = lse;
+            }
+        }
+    }
+    __syncthreads();
+    TO* op = reinterpret_cast<TO*>(p.o) + b * p.os_b + hq * p.os_h;
+#pragma unroll
+    for (int it = 0; it < 32 * OCH / 64; ++it) {
+        const int id = it * 64 + lane;
+        const int row = id / OCH, c = id % OCH;
+        const int qrow = wq0 + row;
+        if (qrow < p.Sq) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Os + row * D + 8 * (c ^ (row % OCH))));
+    }
 }
 
 // TQ: uint8_t (Q given as codes) or bf16_t / f16_t (Q rounded here); TO: the output element type.
@@ -91,7 +162,15 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
     const int l32 = lane & 31;
     const int hf = lane >> 5;
 
-    const BlockCoord bc = block_coord<CAUSAL>(p.B, p.Hq, p.Hkv, p.group, p.n_qblocks, p.xcd_map);
+    // Pieces are ordered so that piece bid' of tail block tb runs on tb's XCD (n_full, the tail and the
+    // grid are multiples of 8 by the host's plan): the 8 XCDs take blocks round robin.
+    int bid = blockIdx.x, piece = -1;
+    if (!CAUSAL && bid >= p.n_full) {
+        const int j = bid - p.n_full;
+        piece = (j >> 3) % p.tail_s;
+        bid = p.n_full + ((j >> 3) / p.tail_s) * 8 + (j & 7);
+    }
+    const BlockCoord bc = block_coord_at<CAUSAL>(bid, p.B, p.Hq, p.Hkv, p.group, p.n_qblocks, p.xcd_map);
     const int qb = bc.qb, b = bc.b, hq = bc.hq, hk = bc.hk;
 
     const TQ* qp = reinterpret_cast<const TQ*>(p.q) + b * p.qs_b + hq * p.qs_h;
@@ -108,7 +187,12 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
         const int lim = q0 + BM + p.delta;
         kend = lim < 0 ? 0 : (lim < p.Sk ? lim : p.Sk);
     }
-    const int nt = (kend + BN - 1) / BN;
+    int nt = (kend + BN - 1) / BN;
+    int t0 = 0;
+    if (!CAUSAL && piece >= 0) {  // the host's plan leaves every piece at least one tile
+        t0 = piece * p.tail_tiles;
+        nt = min(nt, t0 + p.tail_tiles);
+    }
 
     // Q codes: lane holds query l32, d = ks*64 + hf*32 .. +32.
     i32x8 qf[KSTEPS];
@@ -280,68 +364,196 @@ __global__ void __launch_bounds__(256, 2) prefill_fp8_kernel(const PrefillFp8Par
         }
     };
 
-    if (nt > 0) {
-        dma(Ka, kp, krow, p.ks_s, 0);
-        dma(Va, vp, vrow, p.vs_s, 0);
+    if (nt > t0) {
+        dma(Ka, kp, krow, p.ks_s, t0);
+        dma(Va, vp, vrow, p.vs_s, t0);
     }
     // Q codes (and tile 0) complete here, visibly to the compiler, so that it inserts no load waits
     // inside the loop (where they would also drain the asynchronous tile loads).
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    for (int t = 0; t < nt; t += 2) {  // unrolled by two so each tile names its buffers statically
+    for (int t = t0; t < nt; t += 2) {  // unrolled by two so each tile names its buffers statically
         tile(Ka, Va, Kb, Vb, t);
         if (t + 1 < nt) tile(Kb, Vb, Ka, Va, t + 1);
     }
 
-    // Epilogue: normalise, stage O (16-bit) through LDS -- wave w in the 32 x D slab that is tile
-    // buffer w, 16-byte chunk c of row r at c ^ (r % OCH) -- for 16-byte coalesced row stores, and
-    // write the LSE.
-    typedef typename Elem<TO>::vec4 O4;
-    constexpr int OCH = D / 8;  // 16-byte chunks per 16-bit output row
-    static_assert(32 * D * 2 <= BN * D, "a tile buffer holds one wave's output rows");
-    __syncthreads();
-    TO* Os = reinterpret_cast<TO*>(wave == 0 ? Ka : wave == 1 ? Kb : wave == 2 ? Va : Vb);
-    {
-        const float l = sum_xor32(lrow);
-        const float inv = l > 0.f ? vdesc / l : 0.f;
-        const int row = l32;
+    if (!CAUSAL && piece >= 0) {
+        // A piece stores its O over its own row sum, running max and row sum for fp8_tail_merge_kernel.
+        const float lsum = sum_xor32(lrow);
+        uint8_t* mine = p.tail_part + ((int64_t)(bid - p.n_full) * p.tail_s + piece) * fp8_tail_part_bytes<D>();
+        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+        u32x4* po = reinterpret_cast<u32x4*>(mine) + wave * DT * 2 * 64 + lane;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int i4 = 0; i4 < 4; ++i4) {
-                O4 o4;
+            for (int h = 0; h < 2; ++h) {
+                uint32_t w[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o4[e] = Elem<TO>::from_f32(oacc[dt][4 * i4 + e] * inv);
-                const int c = dt * 4 + i4;
-                *reinterpret_cast<O4*>(Os + row * D + 8 * (c ^ (row % OCH)) + 4 * hf) = o4;
+                for (int e = 0; e < 4; ++e)
+                    w[e] = pack_f16x2(oacc[dt][8 * h + 2 * e] * inv, oacc[dt][8 * h + 2 * e + 1] * inv);
+                po[(dt * 2 + h) * 64] = u32x4{w[0], w[1], w[2], w[3]};
             }
-        if (p.lse != nullptr && hf == 0) {
-            const int qrow = wq0 + row;
-            if (qrow < p.Sq) {
-                const float lse = l > 0.f ? (mrow + __log2f(l) - kPScaleLog2) * kLn2 : kNegInf;
-                p.lse[b * p.lses_b + hq * p.lses_h + qrow] = lse;
-            }
+        reinterpret_cast<f32x2*>(mine + fp8_tail_o_bytes<D>())[wave * 64 + lane] = f32x2{mrow, lsum};
+        return;
+    }
+
+    // Epilogue: wave w stages its rows in the 32 x D slab that is tile buffer w.
+    static_assert(32 * D * 2 <= BN * D, "a tile buffer holds one wave's output rows");
+    __syncthreads();
+    TO* Os = reinterpret_cast<TO*>(wave == 0 ? Ka : wave == 1 ? Kb : wave == 2 ? Va : Vb);
+    fp8_write_rows<D, TO>(p, b, hq, wq0, oacc, mrow, sum_xor32(lrow), vdesc, Os);
+}
+
+// Merges the pieces of the tail blocks: workgroup 4*t + w takes wave w's 32 rows of tail block t, reads
+// the pieces' partials in piece order (so the result does not depend on the order the pieces ran in) and
+// writes the rows as an unsplit workgroup would.  A separate launch: stream order makes every piece's
+// stores visible to it, with no cache maintenance inside the attention kernel.
+template <int D, typename TO>
+__global__ void __launch_bounds__(64) fp8_tail_merge_kernel(const PrefillFp8Params p) {
+    constexpr int DT = D / 32;
+    constexpr int64_t PART = fp8_tail_part_bytes<D>();
+    constexpr int NP = DT * 2;  // 16-byte pairs of 4-value groups per lane
+    __shared__ __attribute__((aligned(16))) TO slab[32 * D];
+    const int tb = blockIdx.x >> 2, wave = blockIdx.x & 3, lane = threadIdx.x;
+    const BlockCoord bc = block_coord_at<false>(p.n_full + tb, p.B, p.Hq, p.Hkv, p.group, p.n_qblocks, p.xcd_map);
+    const uint8_t* blk = p.tail_part + (int64_t)tb * p.tail_s * PART;
+    // Loads are unconditional and batched over every piece (a branch per load would make each wait for the
+    // one before; a loop over pieces would wait once per piece): pieces past tail_s re-read the last
+    // piece's values and get weight 0.
+    const int last = p.tail_s - 1;
+    f32x2 ml[kFp8TailMaxPieces];
+#pragma unroll
+    for (int j = 0; j < kFp8TailMaxPieces; ++j)
+        ml[j] = reinterpret_cast<const f32x2*>(blk + min(j, last) * PART + fp8_tail_o_bytes<D>())[wave * 64 + lane];
+    float mtot = kNegInf;
+#pragma unroll
+    for (int j = 0; j < kFp8TailMaxPieces; ++j) mtot = fmaxf(mtot, ml[j][0]);
+    float c[kFp8TailMaxPieces], ltot = 0.f;  // piece j's share of the row sum
+#pragma unroll
+    for (int j = 0; j < kFp8TailMaxPieces; ++j) {
+        c[j] = j > last || ml[j][0] == kNegInf ? 0.f : fast_exp2(ml[j][0] - mtot) * ml[j][1];
+        ltot += c[j];
+    }
+    f32x16 oacc[DT];
+    constexpr int KC = NP < 4 ? NP : 4;  // pairs per batch: 8 pieces x 4 loads in flight
+#pragma unroll
+    for (int k0 = 0; k0 < NP; k0 += KC) {
+        u32x4 o[kFp8TailMaxPieces][KC];
+#pragma unroll
+        for (int j = 0; j < kFp8TailMaxPieces; ++j) {
+            const u32x4* po = reinterpret_cast<const u32x4*>(blk + min(j, last) * PART) + wave * NP * 64 + lane;
+#pragma unroll
+            for (int q = 0; q < KC; ++q) o[j][q] = po[(k0 + q) * 64];
+        }
+#pragma unroll
+        for (int q = 0; q < KC; ++q) {
+            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < kFp8TailMaxPieces; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const f32x2 v = unpack_f16x2(o[j][q][e]);
+                    acc[2 * e] += c[j] * v[0];
+                    acc[2 * e + 1] += c[j] * v[1];
+                }
+            const int k = k0 + q;  // d tile k / 2, values 8 * (k % 2) .. +7
+#pragma unroll
+            for (int e = 0; e < 8; ++e) oacc[k / 2][8 * (k % 2) + e] = acc[e];
         }
     }
-    __syncthreads();
-    TO* op = reinterpret_cast<TO*>(p.o) + b * p.os_b + hq * p.os_h;
-#pragma unroll
-    for (int it = 0; it < 32 * OCH / 64; ++it) {
-        const int id = it * 64 + lane;
-        const int row = id / OCH, c = id % OCH;
-        const int qrow = wq0 + row;
-        if (qrow < p.Sq) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Os + row * D + 8 * (c ^ (row % OCH))));
+    fp8_write_rows<D, TO>(p, bc.b, bc.hq, bc.qb * 128 + wave * 32, oacc, mtot, ltot, p.vd[bc.b * p.Hkv + bc.hk], slab);
+}
+
+// The tail split of a non-causal launch.  A grid of `blocks` query blocks that is not a whole number of
+// rounds over the GPU's workgroup slots leaves its last round partly empty, and the first round's
+// workgroups end at different times (the oldest workgroup on a CU runs ahead).  The blocks of that
+// last round therefore run as s key pieces each, which the hardware dispatches into whichever slots free
+// up first: s = ceil(slots / tail) pieces (at most 8, at least 4 key tiles each); a second launch
+// merges them.
+struct Fp8TailPlan {
+    int64_t grid;              // workgroups launched
+    int32_t n_full, s, tiles;  // whole blocks; pieces per tail block; key tiles per piece
+    int64_t n_tail;            // tail blocks (0: no split)
+    size_t bytes;              // workspace: the pieces' partials
+};
+
+static Fp8TailPlan fp8_tail_plan(int64_t blocks, int64_t Sk, int64_t D, bool causal, int64_t slots) {
+    Fp8TailPlan t;
+    memset(&t, 0, sizeof(t));
+    t.grid = blocks;
+    t.n_full = (int32_t)(blocks < 0x7fffffff ? blocks : 0x7fffffff);
+    t.s = 1;
+    t.tiles = 1 << 30;
+    const int64_t nt = (Sk + 63) / 64;
+    if (causal || slots <= 0 || slots % 8 != 0 || blocks <= slots || blocks % 8 != 0 || blocks > 0x7fffffff) return t;
+    const int64_t r = blocks % slots;
+    if (r == 0 || 4 * r > 3 * slots) return t;  // no partly empty round, or one nearly full
+    int64_t s = (slots + r - 1) / r;
+    if (s > kFp8TailMaxPieces) s = kFp8TailMaxPieces;
+    if (s > nt / 4) s = nt / 4;
+    if (s < 2) return t;
+    const int64_t tiles = (nt + s - 1) / s;
+    s = (nt + tiles - 1) / tiles;  // every piece gets at least one tile
+    if (s < 2) return t;
+    t.n_full = (int32_t)(blocks - r);
+    t.s = (int32_t)s;
+    t.tiles = (int32_t)tiles;
+    t.n_tail = r;
+    t.grid = t.n_full + r * s;
+    const int64_t part = D == 128 ? fp8_tail_part_bytes<128>() : fp8_tail_part_bytes<64>();
+    t.bytes = (size_t)r * s * part;
+    return t;
+}
+
+// Workgroup slots of the non-causal kernel on `device`: its occupancy per CU times the CUs.  The
+// codes-input instantiation stands for all of them, so that the native path and the codes path split
+// alike (and their results stay bit-identical); 0 when the runtime cannot say.
+static int64_t fp8_slots(int64_t D, int device) {
+    static std::atomic<int> per_cu[2] = {{0}, {0}};
+    std::atomic<int>& c = per_cu[D == 128 ? 1 : 0];
+    int n = c.load(std::memory_order_relaxed);
+    if (n == 0) {
+        const void* fn = D == 128 ? reinterpret_cast<const void*>(&prefill_fp8_kernel<128, false, uint8_t, bf16_t>)
+                                  : reinterpret_cast<const void*>(&prefill_fp8_kernel<64, false, uint8_t, bf16_t>);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 256, 0) != hipSuccess || n < 0) return 0;
+        c.store(n, std::memory_order_relaxed);
     }
+    dtattn_device_peaks pk;
+    if (dtattn_get_device_peaks(device, &pk) != DTATTN_OK) return 0;
+    return (int64_t)n * pk.cu_count;
+}
+
+static Fp8TailPlan fp8_plan_for(const dtattn_prefill_args* a, int device) {
+    const int64_t blocks = (a->Sq + 127) / 128 * a->B * a->Hq;
+    const bool causal = a->causal != 0;
+    return fp8_tail_plan(blocks, a->Sk, a->D, causal, causal ? 0 : fp8_slots(a->D, device));
+}
+
+// Applies `tp` to the kernel parameters when `ws` holds its partials (256-byte aligned); without room
+// the launch runs unsplit.
+static void fp8_apply_plan(PrefillFp8Params& p, const Fp8TailPlan& tp, void* ws, size_t ws_bytes) {
+    if (tp.n_tail == 0 || ws == nullptr || ws_bytes < tp.bytes || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+        return;
+    p.n_full = tp.n_full;
+    p.tail_s = tp.s;
+    p.tail_tiles = tp.tiles;
+    p.tail_part = static_cast<uint8_t*>(ws);
 }
 
 template <int D, bool CAUSAL, typename TQ, typename TO>
 static int launch_fp8(const PrefillFp8Params& prm, hipStream_t stream) {
     PrefillFp8Params p = prm;
     p.n_qblocks = (p.Sq + 127) / 128;
-    const int64_t grid = (int64_t)p.n_qblocks * p.B * p.Hq;
-    if (grid == 0) return DTATTN_OK;
+    const int64_t blocks = (int64_t)p.n_qblocks * p.B * p.Hq;
+    if (blocks == 0) return DTATTN_OK;
+    if (blocks > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill fp8: grid too large");
+    const int64_t grid = p.tail_s > 1 ? p.n_full + (blocks - p.n_full) * p.tail_s : blocks;
+    if (p.tail_s <= 1) p.n_full = (int32_t)blocks;
     if (grid > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill fp8: grid too large");
     hipLaunchKernelGGL((prefill_fp8_kernel<D, CAUSAL, TQ, TO>), dim3((unsigned)grid), dim3(256), 0, stream, p);
-    return check_launch("prefill_fp8_kernel");
+    const int st = check_launch("prefill_fp8_kernel");
+    if (st != DTATTN_OK || CAUSAL || p.tail_s <= 1) return st;
+    hipLaunchKernelGGL((fp8_tail_merge_kernel<D, TO>), dim3((unsigned)((blocks - p.n_full) * 4)), dim3(64), 0, stream, p);
+    return check_launch("fp8_tail_merge_kernel");
 }
 
 template <typename TQ, typename TO>
@@ -381,7 +593,19 @@ static PrefillFp8Params fp8_params(const dtattn_prefill_args* a, float c, int32_
     p.xcd_map = (p.B * p.Hkv) % 8 == 0 ? 1 : 0;
     p.q_and = 0xffffffffu;
     p.q_xor = 0u;
+    p.tail_s = 1;
     return p;
+}
+
+static int stream_device_fp8(hipStream_t stream, int* dev) {
+    return (stream == nullptr ? hipGetDevice(dev) : hipStreamGetDevice(stream, dev)) == hipSuccess ? DTATTN_OK
+                                                                                               : DTATTN_ERR_DEVICE;
+}
+
+// Workspace dtattn_prefill_fwd can use for FP8 codes on `device`: the tail split's (0: none).
+size_t prefill_fp8_workspace_size(const dtattn_prefill_args* a, int device) {
+    if (a->B <= 0 || a->Sq <= 0 || a->Sk <= 0 || (a->D != 64 && a->D != 128)) return 0;
+    return fp8_plan_for(a, device).bytes;
 }
 
 // dtattn_prefill_fwd with FP8 codes: output BF16 or FP16.
@@ -390,6 +614,11 @@ int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, uint32_t q
     PrefillFp8Params p = fp8_params(a, c, delta);
     p.q_and = q_and;
     p.q_xor = q_xor;
+    if (!a->causal && a->workspace != nullptr && a->Sk > 0 && (a->D == 64 || a->D == 128)) {
+        int dev = 0;
+        if (stream_device_fp8(stream, &dev) != DTATTN_OK) return fail(DTATTN_ERR_DEVICE, "prefill fp8: stream device");
+        fp8_apply_plan(p, fp8_plan_for(a, dev), a->workspace, a->workspace_bytes);
+    }
     const bool causal = a->causal != 0;
     if (a->o_dtype == DTATTN_FP16) return dispatch_fp8<uint8_t, f16_t>(p, a->D, causal, stream);
     return dispatch_fp8<uint8_t, bf16_t>(p, a->D, causal, stream);
@@ -399,8 +628,9 @@ int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, uint32_t q
 // factor, k and v descales) and the slice maxima of the three tensors, each region 256-byte aligned.
 struct Fp8Workspace {
     size_t k8, v8, qd, qinv, kd, vd, qpart, kpart, vpart, total;
+    size_t tail, tail_bytes;  // the tail split's region (after total; optional)
 };
-static Fp8Workspace fp8_workspace(const dtattn_prefill_args* a) {
+static Fp8Workspace fp8_workspace(const dtattn_prefill_args* a, int device) {
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     Fp8Workspace w;
     size_t off = 0;
@@ -415,6 +645,8 @@ static Fp8Workspace fp8_workspace(const dtattn_prefill_args* a) {
     w.kpart = off, off += up((size_t)a->B * a->Hkv * quant_slices(a->Sk) * 4);
     w.vpart = off, off += up((size_t)a->B * a->Hkv * quant_slices(a->Sk) * 4);
     w.total = off;
+    w.tail = off;
+    w.tail_bytes = a->Sk > 0 && a->Sq > 0 && device >= 0 ? fp8_plan_for(a, device).bytes : 0;
     return w;
 }
 
@@ -424,7 +656,10 @@ using namespace dtattn;
 
 extern "C" size_t dtattn_prefill_fp8_workspace_size(const dtattn_prefill_args* a) {
     if (a == nullptr || a->B <= 0 || a->Hq <= 0 || a->Hkv <= 0 || a->Sq < 0 || a->Sk < 0 || a->D <= 0) return 0;
-    return fp8_workspace(a).total;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    const Fp8Workspace w = fp8_workspace(a, a->D == 64 || a->D == 128 ? dev : -1);
+    return w.total + w.tail_bytes;
 }
 
 extern "C" int dtattn_prefill_fp8(const dtattn_prefill_args* a, void* stream_) {
@@ -456,7 +691,9 @@ extern "C" int dtattn_prefill_fp8(const dtattn_prefill_args* a, void* stream_) {
     ScalePlan sp;
     const int sst = plan_scale(a->scale, a->D, kSign16, &sp);  // q is rounded from its 16-bit rows
     if (sst != DTATTN_OK) return sst;
-    const Fp8Workspace w = fp8_workspace(a);
+    int dev = 0;
+    if (stream_device_fp8(stream, &dev) != DTATTN_OK) return fail(DTATTN_ERR_DEVICE, "prefill_fp8: stream device");
+    const Fp8Workspace w = fp8_workspace(a, dev);
     if (a->workspace == nullptr || a->workspace_bytes < w.total || (reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
         return fail(DTATTN_ERR_WORKSPACE, "prefill_fp8: a 256-byte aligned workspace of %zu bytes is required, %zu given",
                     w.total, a->workspace_bytes);
@@ -505,6 +742,10 @@ extern "C" int dtattn_prefill_fp8(const dtattn_prefill_args* a, void* stream_) {
     p.q_and = sp.q_and;
     p.q_xor = sp.q_xor;
     const bool causal = a->causal != 0;
+    if (!causal && a->Sk > 0) {
+        const size_t room = a->workspace_bytes - w.tail;
+        fp8_apply_plan(p, fp8_plan_for(a, dev), ws + w.tail, room);
+    }
     if (a->dtype == DTATTN_BF16) return dispatch_fp8<bf16_t, bf16_t>(p, a->D, causal, stream);
     return dispatch_fp8<f16_t, f16_t>(p, a->D, causal, stream);
 }

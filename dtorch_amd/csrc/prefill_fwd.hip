@@ -392,6 +392,7 @@ static int dispatch_prefill(const PrefillParams& p, int D, bool causal, bool pad
 
 int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, uint32_t q_and, uint32_t q_xor,
                 hipStream_t stream);
+size_t prefill_fp8_workspace_size(const dtattn_prefill_args* a, int device);
 int prefill_f32(const PrefillParams& p, int D, bool causal, hipStream_t stream);
 int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, bool pad, hipStream_t stream);
 int wide_key_splits(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int D, int cu_count);
@@ -607,6 +608,7 @@ extern "C" size_t dtattn_prefill_workspace_size(const dtattn_prefill_args* a) {
     if (a == nullptr) return 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (a->dtype == DTATTN_FP8_E4M3FN) return prefill_fp8_workspace_size(a, dev);
     size_t bytes = 0, lse_off = 0;
     wide_plan(a, dev, &bytes, &lse_off);
     return bytes;

@@ -93,8 +93,11 @@ typedef struct {
     int64_t mask_stride[3];
     /* Optional workspace (ABI version 7; NULL / 0: none).  Wide heads (a kernel head dim of 256 or 512)
      * whose grid would leave CUs idle run the keys as several blocks in one launch and merge them by
-     * LSE; the blocks' partial outputs live here.  dtattn_prefill_workspace_size() says how much a call
-     * can use; with less, the call runs unsplit (same results up to the rounding of the partials). */
+     * LSE; the blocks' partial outputs live here.  Non-causal FP8 calls whose grid ends in a partly
+     * empty round over the GPU's workgroup slots run that round's query blocks as key pieces, merged by
+     * a second launch; their partials live here.  dtattn_prefill_workspace_size() says
+     * how much a call can use; with less, the call runs unsplit (same results up to the rounding of the
+     * partials). */
     void* workspace;
     size_t workspace_bytes;
 } dtattn_prefill_args;
@@ -110,9 +113,12 @@ size_t dtattn_prefill_workspace_size(const dtattn_prefill_args* args);
  * which takes fp16 and bf16).  q, k and v are quantized per (b, head) to e4m3fn as
  * dtattn_fp8_quantize_per_head does (absmax scaling, round to nearest even), the attention runs on fp8
  * MFMA with fp32 accumulation, and the output has the inputs' dtype.  args: dtype BF16 or FP16, o_dtype
- * equal to it, D == Dv in {64, 128}, no mask; `workspace` of dtattn_prefill_fp8_workspace_size() bytes,
- * 256-byte aligned (K/V codes, scales, partial maxima).  Three launches: the per-head maxima of q, k and
- * v; the K/V codes and every scale; the attention, which rounds its own Q rows to e4m3 in registers. */
+ * equal to it, D == Dv in {64, 128}, no mask; `workspace` of dtattn_prefill_fp8_workspace_size() bytes
+ * (on the current device), 256-byte aligned: K/V codes, scales, partial maxima, then the tail split's
+ * partials as for FP8 codes in dtattn_prefill_fwd (optional: a workspace that ends before them runs
+ * unsplit).  Three launches: the per-head maxima of q, k and v; the K/V codes and every scale; the
+ * attention, which rounds its own Q rows to e4m3 in registers (and a fourth, merging the split's pieces,
+ * when the split runs). */
 size_t dtattn_prefill_fp8_workspace_size(const dtattn_prefill_args* args);
 int dtattn_prefill_fp8(const dtattn_prefill_args* args, void* stream);
 

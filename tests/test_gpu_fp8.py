@@ -197,3 +197,59 @@ def test_native_fp8_empty_keys_and_errors():
     y = torch.randn(1, 2, 16, 128, device="cuda", dtype=torch.float32)
     with pytest.raises(ValueError, match="bf16 or fp16"):
         F.scaled_dot_product_attention(y, y, y, sdpa_option=opt)
+
+
+def _prefill_ws_bytes(q8, k8, causal):
+    """dtattn_prefill_workspace_size for FP8 codes of these shapes on the current device."""
+    import ctypes
+    from dtorch_amd import _lib
+    a = _lib.PrefillArgs()
+    a.B, a.Hq, a.Sq, a.D = q8.shape
+    a.Hkv, a.Sk, a.Dv = k8.shape[1], k8.shape[2], q8.shape[3]
+    a.dtype, a.o_dtype, a.causal = 2, 0, int(causal)
+    lib = _lib.cabi()
+    lib.dtattn_prefill_workspace_size.argtypes = [ctypes.c_void_p]
+    lib.dtattn_prefill_workspace_size.restype = ctypes.c_size_t
+    return lib.dtattn_prefill_workspace_size(ctypes.byref(a))
+
+
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D", [
+    (32, 8, 3300, 2100, 128),   # 832 query blocks over 768 slots: 64 tail blocks in 7 pieces of 5 tiles
+    (16, 16, 8704, 2100, 64),   # D = 64 (4 workgroups per CU, 1,024 slots): 64 tail blocks
+])
+def test_fp8_tail_split(Hq, Hkv, Sq, Sk, D):
+    # Non-causal grids that end in a partly empty round run their last query blocks as key pieces merged
+    # in the kernel.  Checked: the split is planned on this GPU, its rows (tail blocks and whole ones)
+    # against the oracle on the dequantized inputs, the run-to-run determinism of the merge, the unsplit
+    # call within the kernel bar, and the fused native path bit-identical to the codes path.
+    from dtorch_amd import _lib
+    F = _F()
+    g = torch.Generator(device="cuda").manual_seed(Sq + D)
+    q = torch.randn(1, Hq, Sq, D, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(1, Hkv, Sk, D, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(1, Hkv, Sk, D, generator=g, device="cuda").to(torch.bfloat16)
+    (q8, qd), (k8, kd), (v8, vd) = (F.quantize_fp8_per_head(x) for x in (q, k, v))
+    props = torch.cuda.get_device_properties(0)
+    if props.multi_processor_count != 256:
+        pytest.skip(f"the shapes are sized for 256 CUs ({props.multi_processor_count} here)")
+    assert _prefill_ws_bytes(q8, k8, False) > 0, "no tail split planned"
+    assert _prefill_ws_bytes(q8, k8, True) == 0
+    o, lse = _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, torch.bfloat16)
+    o2, lse2 = _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, torch.bfloat16)
+    ou, lseu = _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, torch.bfloat16, split=False)
+    fo, flse = F.scaled_dot_product_attention_with_lse(q, k, v, enable_gqa=Hq != Hkv,
+                                                       sdpa_option=F.SdpaOption(sage_attn_type="native_fp8"))
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert torch.equal(fo, o) and torch.equal(flse, lse)
+    assert not torch.equal(o, ou)  # the split ran
+    assert float((o.float() - ou.float()).abs().max()) <= O_TOL_FP8_KERNEL
+    # rows of the tail blocks (the plain grid's last 64 query blocks: the last two or four query block
+    # ranks of every head), of a whole block, and the ragged last rows
+    rows = np.array([0, 77, 3000, 3100, 3299] if Sq == 3300 else [5, 4000, 8191, 8300, 8703])
+    dq = orc.fp8_dequantize_per_head(q8.view(torch.uint8).cpu().numpy()[:, :, rows], qd.cpu().numpy())
+    dk = orc.fp8_dequantize_per_head(k8.view(torch.uint8).cpu().numpy(), kd.cpu().numpy())
+    dv = orc.fp8_dequantize_per_head(v8.view(torch.uint8).cpu().numpy(), vd.cpu().numpy())
+    ro, rl = orc.sdpa_fwd(dq, dk, dv, enable_gqa=Hq != Hkv)
+    assert max_abs(host(o[:, :, rows]), ro) <= O_TOL_FP8_KERNEL
+    assert lse_rel(host(lse[:, :, rows]), rl) <= LSE_TOL

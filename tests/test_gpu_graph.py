@@ -2,7 +2,8 @@
 then replayed with new inputs.  Every replay must equal the eager step bit for bit: the kernels allocate
 nothing, clear nothing with memset, and read the sequence lengths from device memory, so a replay appends
 at the current length and advances it.  The prefill entry points (causal GQA, wide heads with key blocks and
-their merge, a mask, native fp8 in three launches, the ring step) captured the same way.  Eager work and
+their merge, a mask, native fp8 in three launches and in four with its tail split, the ring step) captured
+the same way.  Eager work and
 synchronisations run between the replays.
 """
 import numpy as np
@@ -52,19 +53,22 @@ def test_decode_step_graph_replays_match_eager(dtype):
     assert cache._span() == T
 
 
-@pytest.mark.parametrize("case", ["causal_gqa", "wide_key_blocks", "masked", "native_fp8", "ring_step"])
+@pytest.mark.parametrize("case", ["causal_gqa", "wide_key_blocks", "masked", "native_fp8", "native_fp8_tail",
+                                  "ring_step"])
 def test_prefill_graph_replays_match_eager(case):
     # The prefill entry points under capture, replayed with new inputs copied into the captured tensors:
     # every replay equals the eager call bit for bit.  The wide-head case takes the key-block split, so its
-    # workspace and the LSE merge launch are captured too.
+    # workspace and the LSE merge launch are captured too; the fp8 tail case (832 query blocks over 768 slots)
+    # takes the tail split and its merge launch.
     import dtorch_amd.nn.functional as F
     rng = np.random.default_rng(sum(map(ord, case)))
     shapes = {"causal_gqa": (2, 8, 2, 300, 300, 128), "wide_key_blocks": (1, 2, 1, 256, 2048, 512),
               "masked": (1, 4, 4, 200, 260, 64), "native_fp8": (1, 4, 2, 256, 256, 128),
+              "native_fp8_tail": (1, 32, 8, 3300, 2100, 128),
               "ring_step": (1, 4, 2, 128, 256, 128)}  # a 128-row Q chunk against two 128-key chunks
     B, Hq, Hkv, Sq, Sk, D = shapes[case]
     mask = torch.from_numpy(rng.random((Sq, Sk)) < 0.7).cuda() if case == "masked" else None
-    opt = F.SdpaOption(sage_attn_type="native_fp8") if case == "native_fp8" else F.SdpaOption()
+    opt = F.SdpaOption(sage_attn_type="native_fp8") if case.startswith("native_fp8") else F.SdpaOption()
 
     def call(q, k, v):
         if case == "ring_step":
