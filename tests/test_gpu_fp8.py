@@ -213,11 +213,12 @@ def _prefill_ws_bytes(q8, k8, causal):
     return lib.dtattn_prefill_workspace_size(ctypes.byref(a))
 
 
-@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D", [
-    (32, 8, 3300, 2100, 128),   # 832 query blocks over 768 slots: 64 tail blocks in 7 pieces of 5 tiles
-    (16, 16, 8704, 2100, 64),   # D = 64 (4 workgroups per CU, 1,024 slots): 64 tail blocks
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,dtype", [
+    (32, 8, 3300, 2100, 128, torch.bfloat16),  # 832 query blocks over 768 slots: 64 tail blocks in 7 pieces
+    (32, 8, 3300, 2100, 128, torch.float16),   # the fp16 output of the merge
+    (16, 16, 8704, 2100, 64, torch.bfloat16),  # D = 64 (4 workgroups per CU, 1,024 slots): 64 tail blocks
 ])
-def test_fp8_tail_split(Hq, Hkv, Sq, Sk, D):
+def test_fp8_tail_split(Hq, Hkv, Sq, Sk, D, dtype):
     # Non-causal grids that end in a partly empty round run their last query blocks as key pieces merged
     # in the kernel.  Checked: the split is planned on this GPU, its rows (tail blocks and whole ones)
     # against the oracle on the dequantized inputs, the run-to-run determinism of the merge, the unsplit
@@ -225,21 +226,22 @@ def test_fp8_tail_split(Hq, Hkv, Sq, Sk, D):
     from dtorch_amd import _lib
     F = _F()
     g = torch.Generator(device="cuda").manual_seed(Sq + D)
-    q = torch.randn(1, Hq, Sq, D, generator=g, device="cuda").to(torch.bfloat16)
-    k = torch.randn(1, Hkv, Sk, D, generator=g, device="cuda").to(torch.bfloat16)
-    v = torch.randn(1, Hkv, Sk, D, generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randn(1, Hq, Sq, D, generator=g, device="cuda").to(dtype)
+    k = torch.randn(1, Hkv, Sk, D, generator=g, device="cuda").to(dtype)
+    v = torch.randn(1, Hkv, Sk, D, generator=g, device="cuda").to(dtype)
     (q8, qd), (k8, kd), (v8, vd) = (F.quantize_fp8_per_head(x) for x in (q, k, v))
     props = torch.cuda.get_device_properties(0)
     if props.multi_processor_count != 256:
         pytest.skip(f"the shapes are sized for 256 CUs ({props.multi_processor_count} here)")
     assert _prefill_ws_bytes(q8, k8, False) > 0, "no tail split planned"
     assert _prefill_ws_bytes(q8, k8, True) == 0
-    o, lse = _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, torch.bfloat16)
-    o2, lse2 = _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, torch.bfloat16)
-    ou, lseu = _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, torch.bfloat16, split=False)
+    o, lse = _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, dtype)
+    o2, lse2 = _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, dtype)
+    ou, lseu = _lib.prefill_fp8_codes(q8, k8, v8, qd, kd, vd, dtype, split=False)
     fo, flse = F.scaled_dot_product_attention_with_lse(q, k, v, enable_gqa=Hq != Hkv,
                                                        sdpa_option=F.SdpaOption(sage_attn_type="native_fp8"))
     torch.cuda.synchronize()
+    assert o.dtype == dtype and fo.dtype == dtype
     assert torch.equal(o, o2) and torch.equal(lse, lse2)
     assert torch.equal(fo, o) and torch.equal(flse, lse)
     assert not torch.equal(o, ou)  # the split ran
