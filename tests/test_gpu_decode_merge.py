@@ -326,6 +326,30 @@ def test_decode_paged_fp16_and_errors():
         F.decode_attention_paged(to_dev(q, torch.float16), tk, tv, tb.long(), tl)
 
 
+def test_decode_paged_16_token_pages_fp16():
+    # 16-token pages of fp16 rows take the path that loads each wave's page ids up front: the sequences'
+    # last chunks read table slots past their last page (an id far outside the pool) and rows past their
+    # end (NaN), which must not reach the result; bit-identical to the contiguous decode
+    rng = np.random.default_rng(23)
+    lengths = np.array([1, 383, 384, 385, 1500, 0, 770], dtype=np.int32)
+    B, Hq, Hkv, D, ps = len(lengths), 16, 4, 128, 16
+    q = randn(rng, (B, Hq, 1, D))
+    kp, vp, tk, tv, bt, max_pages = _paged_pool(rng, lengths, Hkv, D, ps, dtype=torch.float16)
+    F = _F()
+    tq, tl = to_dev(q, torch.float16), torch.from_numpy(lengths).cuda()
+    o, lse = F.decode_attention_paged(tq, tk, tv, torch.from_numpy(bt).cuda(), tl)
+    S = max_pages * ps
+    co, cl = F.decode_attention(tq, _gather_dev(tk, bt, lengths, S), _gather_dev(tv, bt, lengths, S), tl)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all()
+    assert torch.equal(o, co) and torch.equal(lse, cl)
+    nz = np.flatnonzero(lengths > 0)
+    ro, rl = orc.decode_paged(rounded(q[nz], torch.float16), rounded(np.nan_to_num(kp), torch.float16),
+                              rounded(np.nan_to_num(vp), torch.float16), bt[nz], lengths[nz])
+    assert max_abs(host(o)[nz], ro) <= O_TOL_BF16
+    assert lse_rel(host(lse)[nz], rl[..., 0]) <= LSE_TOL
+
+
 def test_config3_decode_paged_full_size():
     # the full-size decode workload (B=64, Hq=32, Hkv=8, D=128, lengths ~ U[512, 8192]) in 16-token
     # pages scattered over the pool: bit-identical to the contiguous decode over the gathered cache,
