@@ -133,7 +133,9 @@ __device__ __forceinline__ void fp8_write_rows(const PrefillFp8Params& p, int b,
         const int id = it * 64 + lane;
         const int row = id / OCH, c = id % OCH;
         const int qrow = wq0 + row;
-        if (qrow < p.Sq) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Os + row * D + 8 * (c ^ (row % OCH))));
+        if (qrow < p.Sq)
+            __builtin_nontemporal_store(ld16(Os + row * D + 8 * (c ^ (row % OCH))),
+                                        reinterpret_cast<u32x4*>(op + (int64_t)qrow * p.os_s + c * 8));
     }
 }
 

@@ -349,7 +349,11 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
         const int id = it * 64 + lane;
         const int row = id / DCH, c = id % DCH;
         const int qrow = wq0 + row;
-        if (qrow < p.Sq && (!PAD || c < p.v_ch)) st16(op + (int64_t)qrow * p.os_s + c * 8, ld16(Os + row * D + 8 * (c ^ (row % DCH))));
+        // non-temporal: measured +1.3 to 2.5% on short sequences (16x512, 32x256), +0.2 to 0.3% on long ones,
+        // against plain stores, with back-to-back launches
+        if (qrow < p.Sq && (!PAD || c < p.v_ch))
+            __builtin_nontemporal_store(ld16(Os + row * D + 8 * (c ^ (row % DCH))),
+                                        reinterpret_cast<u32x4*>(op + (int64_t)qrow * p.os_s + c * 8));
     }
 }
 
