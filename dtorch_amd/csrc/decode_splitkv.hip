@@ -82,8 +82,8 @@ size_t decode_ws_parts(int64_t B, int64_t Hq, int64_t S_max, int64_t D_real, int
 // all trip counts are compile-time so each sub-block's loads issue together).
 // PAGED: 0, rows of a contiguous cache through a buffer resource over the chunk's rows; 1, rows of a paged
 // cache through the block table, with 64-bit loads of clamped token indices; 2, the same through a buffer
-// resource over the kv head's pages with 32-bit offsets, when they fit (DecodeParams::kspan); 3 and 4, as 2
-// for 16- and 32-token pages of 16-bit rows, with each wave's page ids in scalar registers (loaded with
+// resource over the kv head's pages with 32-bit offsets, when they fit (DecodeParams::kspan); 3, 4 and 5, as
+// 2 for 16-, 32- and larger pages of 16-bit rows, with each wave's page ids in scalar registers (loaded with
 // lengths[b]);
 // otherwise through a buffer resource over the chunk's rows.
 // The sub-block loop of one fp32 instantiation (three 32-token sub-blocks per wave) is too large to
@@ -116,18 +116,23 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     const int sg = blockIdx.x / p.Hkv;   // head subgroup within the kv group
     const int b = blockIdx.y;
     const int t0 = split * C;
-    // PAGED >= 3 (16- or 32-token pages, 16-bit rows): the wave's page ids are scalar loads issued together
-    // with lengths[b] (the empty asm keeps the compiler from sinking them past the exits below), so the
-    // cache loads follow lengths by one round trip, as in the contiguous kernel, instead of two.
-    constexpr int PSH = PAGED == 4 ? 5 : 4;  // log2 of the page size
-    constexpr int NPW = PAGED >= 3 ? TPW >> PSH : 1;
-    static_assert(PAGED < 3 || (TPW % (1 << PSH) == 0 && (1 << PSH) % TPI == 0), "whole pages per wave");
+    // PAGED >= 3 (16-bit rows): the wave's page ids are scalar loads issued together with lengths[b] (the
+    // empty asm keeps the compiler from sinking them past the exits below), so the cache loads follow
+    // lengths by one round trip, as in the contiguous kernel, instead of two.  16- and 32-token pages
+    // (3, 4): a wave's tokens are whole pages.  Pages of 64 tokens or more (5): a wave's tokens start
+    // anywhere in a page and span at most 3 of them.
+    constexpr int PSH = PAGED == 4 ? 5 : 4;  // log2 of the page size (3, 4)
+    constexpr int NPW = PAGED == 5 ? 3 : (PAGED >= 3 ? TPW >> PSH : 1);
+    static_assert(PAGED < 3 || PAGED == 5 || (TPW % (1 << PSH) == 0 && (1 << PSH) % TPI == 0), "whole pages per wave");
+    static_assert(PAGED != 5 || (TPW <= 128 && 64 % TPI == 0), "a wave spans at most 3 pages of 64+ tokens");
+    const int sh = PAGED == 5 ? p.page_shift : PSH;
+    const int wbase = t0 + __builtin_amdgcn_readfirstlane(tid >> 6) * TPW;  // the wave's first token
     int pgw[NPW];
     int Lraw;
     if constexpr (PAGED >= 3) {
         typedef const __attribute__((address_space(4))) int32_t cint32;
-        const int pb = (t0 + __builtin_amdgcn_readfirstlane(tid >> 6) * TPW) >> PSH;
-        const int plast = (p.S_max >> PSH) - 1;  // the table row holds S_max / page_size pages
+        const int pb = wbase >> sh;
+        const int plast = (p.S_max >> sh) - 1;  // the table row holds S_max / page_size pages
         cint32* btc = (cint32*)(p.block_table + (int64_t)b * p.bt_s);
 #pragma unroll
         for (int j = 0; j < NPW; ++j) pgw[j] = btc[min(pb + j, plast)];
@@ -188,7 +193,7 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
         u32x4 kr[NI], vr[NI];
         if constexpr (PAGED >= 3) {
             // Load i covers tokens base + sb*SB + i*TPI + tsub of one page, the wave's page
-            // (sb*SB + i*TPI) / page_size.  Pages past the sequence end hold any id: clamped to the pool, their
+            // (sb*SB + i*TPI) / page_size (3, 4), or its page (base + sb*SB + i*TPI) / page_size (5).  Pages past the sequence end hold any id: clamped to the pool, their
             // rows are read but get score -inf and V = 0 below.
             const auto kprs = make_rsrc(kp, p.kspan);
             const auto vprs = make_rsrc(vp, p.vspan);
@@ -196,9 +201,18 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
             const uint32_t vpb = (uint32_t)(p.vs_b * sizeof(T)), vps = (uint32_t)(p.vs_s * sizeof(T));
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
-                const int j = (sb * SB + i * TPI) >> PSH;
-                const uint32_t pg = (uint32_t)min(max(pgw[j], 0), p.num_pages - 1);
-                const uint32_t row = (uint32_t)((sb * SB + i * TPI + tsub) & ((1 << PSH) - 1));
+                int page_id, rowi;
+                if constexpr (PAGED == 5) {
+                    const int tok = wbase + sb * SB + i * TPI;  // wave-uniform
+                    const int j = (tok >> sh) - (wbase >> sh);
+                    page_id = j == 0 ? pgw[0] : (j == 1 ? pgw[1] : pgw[2]);
+                    rowi = (tok & ((1 << sh) - 1)) + tsub;
+                } else {
+                    page_id = pgw[(sb * SB + i * TPI) >> PSH];
+                    rowi = (sb * SB + i * TPI + tsub) & ((1 << PSH) - 1);
+                }
+                const uint32_t pg = (uint32_t)min(max(page_id, 0), p.num_pages - 1);
+                const uint32_t row = (uint32_t)rowi;
                 kr[i] = buf_ld16_nt(kprs, pg * kpb + row * kps + (uint32_t)c8 * 16u);
                 vr[i] = buf_ld16_nt(vprs, pg * vpb + row * vps + (uint32_t)c8 * 16u);
             }
@@ -721,6 +735,10 @@ extern "C" int dtattn_decode_paged(const dtattn_decode_paged_args* a, void* stre
     if (p.kspan != 0 && a->page_size == 32 && a->dtype != DTATTN_FP32) {
         if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, 4>(p, (int)a->D, stream);
         return dispatch_decode<f16_t, 4>(p, (int)a->D, stream);
+    }
+    if (p.kspan != 0 && a->page_size >= 64 && a->dtype != DTATTN_FP32) {
+        if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, 5>(p, (int)a->D, stream);
+        return dispatch_decode<f16_t, 5>(p, (int)a->D, stream);
     }
     if (p.kspan != 0) {
         if (a->dtype == DTATTN_BF16) return dispatch_decode<bf16_t, 2>(p, (int)a->D, stream);

@@ -178,9 +178,9 @@ int dtattn_decode_splitkv_noalloc(const dtattn_decode_args* args, void* stream);
  * decode operator, python/dtorch/test/modules/llama.py:126-156).  Same arithmetic as
  * dtattn_decode_splitkv; token t of sequence b lives in page block_table[b][t / page_size] at row
  * t % page_size.  Page ids are clamped to [0, num_pages), so a corrupt block table reads wrong rows
- * but never leaves the pool.  Rows at or past lengths[b] never enter the result; with 16- or 32-token
- * pages of bf16/fp16 rows (and a pool whose kv-head span fits 4 GB) the last chunk of a sequence may read
- * them, and the table entries past its last page, from within the pool and the table.
+ * but never leaves the pool.  Rows at or past lengths[b] never enter the result; with bf16/fp16 rows
+ * (and a pool whose kv-head span fits 4 GB) the last chunk of a sequence may read them, and the table
+ * entries past its last page, from within the pool and the table.
  */
 typedef struct {
     const void* q;             /* [B, Hq, 1, D] */
