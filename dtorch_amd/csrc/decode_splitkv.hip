@@ -192,9 +192,10 @@ __global__ void __launch_bounds__(256) decode_kernel(const DecodeParams p) {
     for (int sb = 0; sb < NSB; ++sb) {
         u32x4 kr[NI], vr[NI];
         if constexpr (PAGED >= 3) {
-            // Load i covers tokens base + sb*SB + i*TPI + tsub of one page, the wave's page
-            // (sb*SB + i*TPI) / page_size (3, 4), or its page (base + sb*SB + i*TPI) / page_size (5).  Pages past the sequence end hold any id: clamped to the pool, their
-            // rows are read but get score -inf and V = 0 below.
+            // Load i covers tokens wbase + sb*SB + i*TPI + tsub, which lie in one page: the wave's page
+            // (sb*SB + i*TPI) / page_size (3, 4), or the one of 3 its token index names (5).  Pages past the
+            // sequence end hold any id: clamped to the pool, their rows are read but get score -inf and
+            // V = 0 below.
             const auto kprs = make_rsrc(kp, p.kspan);
             const auto vprs = make_rsrc(vp, p.vspan);
             const uint32_t kpb = (uint32_t)(p.ks_b * sizeof(T)), kps = (uint32_t)(p.ks_s * sizeof(T));
