@@ -4,7 +4,9 @@
 // Two entry points: dtattn_prefill_fwd with FP8 codes from the caller, and dtattn_prefill_fp8, the
 // native fp8 path from bf16/fp16 inputs in three launches: per-head maxima of q, k and v; K/V codes
 // plus the scales of all three; then this kernel, which rounds its own 128 Q rows to e4m3 in registers
-// with the same per-head factor (so Q's codes never go through memory).
+// with the same per-head factor (so Q's codes never go through memory).  Non-causal grids whose last
+// round over the GPU's workgroup slots is partly empty split that round's query blocks into key pieces,
+// merged by a fourth launch (fp8_tail_merge_kernel) in either entry point.
 //
 // Supersedes the quantized branch of SdpaOp::Compute, which hands q/k/v to the third-party
 // SageAttention package (dtorch/core/operators/standard/scaled_dot_product_attention_op.cc:110-117,
