@@ -213,12 +213,18 @@ def _prefill_ws_bytes(q8, k8, causal):
     return lib.dtattn_prefill_workspace_size(ctypes.byref(a))
 
 
-@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,dtype", [
-    (32, 8, 3300, 2100, 128, torch.bfloat16),  # 832 query blocks over 768 slots: 64 tail blocks in 7 pieces
-    (32, 8, 3300, 2100, 128, torch.float16),   # the fp16 output of the merge
-    (16, 16, 8704, 2100, 64, torch.bfloat16),  # D = 64 (4 workgroups per CU, 1,024 slots): 64 tail blocks
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D,dtype,rows", [
+    # 832 query blocks over 768 slots: 64 tail blocks (the last two query-block ranks) in 7 pieces
+    (1, 32, 8, 3300, 2100, 128, torch.bfloat16, [0, 77, 3000, 3100, 3299]),
+    (1, 32, 8, 3300, 2100, 128, torch.float16, [0, 77, 3000, 3100, 3299]),   # the fp16 output of the merge
+    # D = 64 (4 workgroups per CU, 1,024 slots): 64 tail blocks
+    (1, 16, 16, 8704, 2100, 64, torch.bfloat16, [5, 4000, 8191, 8300, 8703]),
+    # two sequences, 1,128 blocks: 360 tail blocks (ranks 32-46) in 3 pieces of 14, 14 and 12 tiles
+    (2, 12, 12, 6000, 2500, 128, torch.bfloat16, [100, 4095, 4100, 5000, 5999]),
+    # B * Hkv = 20 is not a multiple of 8 (no XCD grouping of the grid): 32 tail blocks in 8 pieces
+    (1, 20, 20, 5000, 2000, 128, torch.bfloat16, [0, 2500, 4863, 4900, 4999]),
 ])
-def test_fp8_tail_split(Hq, Hkv, Sq, Sk, D, dtype):
+def test_fp8_tail_split(B, Hq, Hkv, Sq, Sk, D, dtype, rows):
     # Non-causal grids that end in a partly empty round run their last query blocks as key pieces merged
     # in the kernel.  Checked: the split is planned on this GPU, its rows (tail blocks and whole ones)
     # against the oracle on the dequantized inputs, the run-to-run determinism of the merge, the unsplit
@@ -226,9 +232,9 @@ def test_fp8_tail_split(Hq, Hkv, Sq, Sk, D, dtype):
     from dtorch_amd import _lib
     F = _F()
     g = torch.Generator(device="cuda").manual_seed(Sq + D)
-    q = torch.randn(1, Hq, Sq, D, generator=g, device="cuda").to(dtype)
-    k = torch.randn(1, Hkv, Sk, D, generator=g, device="cuda").to(dtype)
-    v = torch.randn(1, Hkv, Sk, D, generator=g, device="cuda").to(dtype)
+    q = torch.randn(B, Hq, Sq, D, generator=g, device="cuda").to(dtype)
+    k = torch.randn(B, Hkv, Sk, D, generator=g, device="cuda").to(dtype)
+    v = torch.randn(B, Hkv, Sk, D, generator=g, device="cuda").to(dtype)
     (q8, qd), (k8, kd), (v8, vd) = (F.quantize_fp8_per_head(x) for x in (q, k, v))
     props = torch.cuda.get_device_properties(0)
     if props.multi_processor_count != 256:
@@ -246,9 +252,8 @@ def test_fp8_tail_split(Hq, Hkv, Sq, Sk, D, dtype):
     assert torch.equal(fo, o) and torch.equal(flse, lse)
     assert not torch.equal(o, ou)  # the split ran
     assert float((o.float() - ou.float()).abs().max()) <= O_TOL_FP8_KERNEL
-    # rows of the tail blocks (the plain grid's last 64 query blocks: the last two or four query block
-    # ranks of every head), of a whole block, and the ragged last rows
-    rows = np.array([0, 77, 3000, 3100, 3299] if Sq == 3300 else [5, 4000, 8191, 8300, 8703])
+    # rows of the tail blocks, of whole blocks, and the ragged last rows
+    rows = np.array(rows)
     dq = orc.fp8_dequantize_per_head(q8.view(torch.uint8).cpu().numpy()[:, :, rows], qd.cpu().numpy())
     dk = orc.fp8_dequantize_per_head(k8.view(torch.uint8).cpu().numpy(), kd.cpu().numpy())
     dv = orc.fp8_dequantize_per_head(v8.view(torch.uint8).cpu().numpy(), vd.cpu().numpy())
