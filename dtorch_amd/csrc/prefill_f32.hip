@@ -23,12 +23,16 @@
 // Pipeline per key tile j (one barrier per tile), as in the bf16 kernel:
 //   wait own loads + barrier | K[j+1], V[j+1] -> LDS (async) | S^T = K[j] Q^T | softmax |
 //   O^T += V^T(j) P^T(j)
+//
+// PAD: the real head dims are below the kernel's D (any multiples of 4, Dv may differ from D), as in
+// the bf16 kernel: Q/K chunks past p.qk_ch and V chunks past p.v_ch load as zeros (adding nothing to
+// the scores, giving O columns that are never stored), and O chunks past p.v_ch are not written.
 #include "dtattn_common.hpp"
 #include "prefill_params.hpp"
 
 namespace dtattn {
 
-template <int D, bool CAUSAL, bool MASKED>
+template <int D, bool CAUSAL, bool MASKED, bool PAD>
 __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(const PrefillParams p) {
     constexpr int NW = 4;
     constexpr int BN = 32;           // keys per tile
@@ -82,18 +86,23 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(const PrefillParams
 
     // Tile t -> LDS by direct buffer->LDS loads: one wave instruction fills 1 KB (lane l -> byte 16*l),
     // i.e. 1024 / (4 D) rows; lane l loads the global chunk that belongs at its LDS slot,
-    // c = slot ^ (row & 15).  The buffer resource covers the tile's valid rows; rows past Sk read zeros.
-    auto dma = [&](float* dst, const float* base, int pitch, int64_t stride, int t) {
+    // c = slot ^ (row & 15).  The buffer resource covers the tile's valid rows; rows past Sk read zeros,
+    // and so do chunks at or past valid_ch (PAD), whose offset lies past the resource.
+    auto dma = [&](float* dst, const float* base, int pitch, int64_t stride, int t, int valid_ch) {
         constexpr int ROWS_PER_INSTR = 1024 / (4 * D);
         constexpr int INSTR = BN / ROWS_PER_INSTR / NW;  // per wave
         const int rows = min(BN, p.Sk - t * BN);
-        const auto rs = make_rsrc(base + (int64_t)t * BN * stride, (uint32_t)((rows - 1) * pitch + D * 4));
+        // the resource ends where the tile's last valid row ends (its real width under PAD)
+        const uint32_t nbytes = (uint32_t)((rows - 1) * pitch + (PAD ? valid_ch * 16 : D * 4));
+        const auto rs = make_rsrc(base + (int64_t)t * BN * stride, nbytes);
 #pragma unroll
         for (int i = 0; i < INSTR; ++i) {
             const int r0 = (wave * INSTR + i) * ROWS_PER_INSTR;
             const int r = r0 + lane / DCH;
             const int c = (lane % DCH) ^ (r & 15);
-            buf_ld16_lds_async(rs, dst + r0 * D, (uint32_t)(r * pitch + c * 16));
+            // 2^31 lies past every tile's resource (the host keeps 64 row pitches below 2^31)
+            const uint32_t off = (PAD && c >= valid_ch) ? 0x80000000u : (uint32_t)(r * pitch + c * 16);
+            buf_ld16_lds_async(rs, dst + r0 * D, off);
         }
     };
 
@@ -109,8 +118,8 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(const PrefillParams
         lds_barrier();  // tile t landed everywhere; every wave finished tile t-1 (so Kn/Vn are free)
         auto next_tile = [&]() {
             if (t + 1 < nt) {
-                dma(Kn, kp, krow, p.ks_s, t + 1);
-                dma(Vn, vp, vrow, p.vs_s, t + 1);
+                dma(Kn, kp, krow, p.ks_s, t + 1, p.qk_ch);
+                dma(Vn, vp, vrow, p.vs_s, t + 1, p.v_ch);
             }
         };
         if constexpr (!MASKED) next_tile();
@@ -219,19 +228,22 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(const PrefillParams
     };
 
     if (nt > 0) {
-        dma(Ka, kp, krow, p.ks_s, 0);
-        dma(Va, vp, vrow, p.vs_s, 0);
+        dma(Ka, kp, krow, p.ks_s, 0, p.qk_ch);
+        dma(Va, vp, vrow, p.vs_s, 0, p.v_ch);
     }
     // Lane (l32, hf) holds Q[wq0 + l32][HD*hf + s], s < HD.  Unconditional loads issue back to back and
     // share the first tile's memory latency (a branch per load serialised them); rows past Sq read row
-    // Sq-1 and are zeroed by the mask.
+    // Sq-1 and are zeroed by the mask; so are chunks at or past qk_ch (PAD), which read chunk 0.
     {
         const int qrow = wq0 + l32;
         const bool row_ok = qrow < p.Sq;
-        const float* qsrc = qp + (int64_t)(row_ok ? qrow : p.Sq - 1) * p.qs_s + HD * hf;
+        const float* qsrc = qp + (int64_t)(row_ok ? qrow : p.Sq - 1) * p.qs_s;
 #pragma unroll
         for (int g = 0; g < HD / 4; ++g) {
-            const u32x4 raw = q_bits(ld16(qsrc + 4 * g), row_ok ? p.q_and : 0u, row_ok ? p.q_xor : 0u);
+            const int ch = (HD / 4) * hf + g;  // 16-byte chunk of the row
+            const bool ok = row_ok && (!PAD || ch < p.qk_ch);
+            const float* src = (!PAD || ch < p.qk_ch) ? qsrc + 4 * ch : qsrc;
+            const u32x4 raw = q_bits(ld16(src), ok ? p.q_and : 0u, ok ? p.q_xor : 0u);
             const f32x4 x = __builtin_bit_cast(f32x4, raw);
             qf[4 * g + 0] = x.x, qf[4 * g + 1] = x.y, qf[4 * g + 2] = x.z, qf[4 * g + 3] = x.w;
         }
@@ -256,14 +268,15 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(const PrefillParams
             fvec o;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o[dt] = oacc[dt][i] * inv;
-            *reinterpret_cast<fvec*>(orow + DT * (8 * (i >> 2) + 4 * hf + (i & 3))) = o;
+            const int col = DT * (8 * (i >> 2) + 4 * hf + (i & 3));  // DT <= 4 floats within one 16-byte chunk
+            if (!PAD || col < 4 * p.v_ch) *reinterpret_cast<fvec*>(orow + col) = o;
         }
         if (p.lse != nullptr && hf == 0)
             p.lse[b * p.lses_b + hq * p.lses_h + qrow] = l > 0.f ? (mrow + __log2f(l)) * kLn2 : kNegInf;
     }
 }
 
-template <int D, bool CAUSAL, bool MASKED>
+template <int D, bool CAUSAL, bool MASKED, bool PAD>
 static int launch_prefill_f32(const PrefillParams& prm, hipStream_t stream) {
     constexpr int BM = 4 * 32;
     PrefillParams p = prm;
@@ -271,23 +284,29 @@ static int launch_prefill_f32(const PrefillParams& prm, hipStream_t stream) {
     const int64_t grid = (int64_t)p.n_qblocks * p.B * p.Hq;
     if (grid == 0) return DTATTN_OK;
     if (grid > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "prefill grid too large (%lld blocks)", (long long)grid);
-    hipLaunchKernelGGL((prefill_f32_kernel<D, CAUSAL, MASKED>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((prefill_f32_kernel<D, CAUSAL, MASKED, PAD>), dim3((unsigned)grid), dim3(256), 0, stream, p);
     return check_launch("prefill_f32_kernel");
 }
 
-template <bool MASKED>
+template <bool MASKED, bool PAD>
 static int dispatch_prefill_f32_m(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
     if (D == 128)
-        return causal ? launch_prefill_f32<128, true, MASKED>(p, stream) : launch_prefill_f32<128, false, MASKED>(p, stream);
+        return causal ? launch_prefill_f32<128, true, MASKED, PAD>(p, stream)
+                      : launch_prefill_f32<128, false, MASKED, PAD>(p, stream);
     if (D == 64)
-        return causal ? launch_prefill_f32<64, true, MASKED>(p, stream) : launch_prefill_f32<64, false, MASKED>(p, stream);
-    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dim %d not supported (64 or 128)", D);
+        return causal ? launch_prefill_f32<64, true, MASKED, PAD>(p, stream)
+                      : launch_prefill_f32<64, false, MASKED, PAD>(p, stream);
+    return fail(DTATTN_ERR_UNSUPPORTED, "prefill: fp32 kernel head dim %d not supported (64 or 128)", D);
 }
 
-// Entry from dtattn_prefill_fwd once the arguments are validated and `p` is filled.
-int prefill_f32(const PrefillParams& p, int D, bool causal, hipStream_t stream) {
-    return p.mask != nullptr ? dispatch_prefill_f32_m<true>(p, D, causal, stream)
-                             : dispatch_prefill_f32_m<false>(p, D, causal, stream);
+// Entry from dtattn_prefill_fwd once the arguments are validated and `p` is filled.  D is the kernel's
+// head dim (64 or 128); pad: the real head dims (p.qk_ch, p.v_ch chunks of 4 floats) are below it.
+int prefill_f32(const PrefillParams& p, int D, bool causal, bool pad, hipStream_t stream) {
+    if (pad)
+        return p.mask != nullptr ? dispatch_prefill_f32_m<true, true>(p, D, causal, stream)
+                                 : dispatch_prefill_f32_m<false, true>(p, D, causal, stream);
+    return p.mask != nullptr ? dispatch_prefill_f32_m<true, false>(p, D, causal, stream)
+                             : dispatch_prefill_f32_m<false, false>(p, D, causal, stream);
 }
 
 }  // namespace dtattn

@@ -397,7 +397,7 @@ static int dispatch_prefill(const PrefillParams& p, int D, bool causal, bool pad
 int prefill_fp8(const dtattn_prefill_args* a, float c, int32_t delta, uint32_t q_and, uint32_t q_xor,
                 hipStream_t stream);
 size_t prefill_fp8_workspace_size(const dtattn_prefill_args* a, int device);
-int prefill_f32(const PrefillParams& p, int D, bool causal, hipStream_t stream);
+int prefill_f32(const PrefillParams& p, int D, bool causal, bool pad, hipStream_t stream);
 int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, bool pad, hipStream_t stream);
 int wide_key_splits(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int D, int cu_count);
 
@@ -451,12 +451,16 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
         return fail(DTATTN_ERR_INVALID_ARGUMENT, "prefill: bad head dims D=%lld Dv=%lld", (long long)a->D,
                     (long long)a->Dv);
     const bool sixteen_bit = a->dtype == DTATTN_BF16 || a->dtype == DTATTN_FP16;
-    if (a->D != a->Dv && !sixteen_bit)
-        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: D=%lld != Dv=%lld is supported for bf16/fp16 only",
+    if (a->D != a->Dv && !sixteen_bit && a->dtype != DTATTN_FP32)
+        return fail(DTATTN_ERR_UNSUPPORTED, "prefill: D=%lld != Dv=%lld is supported for bf16/fp16/fp32 only",
                     (long long)a->D, (long long)a->Dv);
     if (sixteen_bit && (a->D % 8 != 0 || a->Dv % 8 != 0))
         return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dims must be multiples of 8 (D=%lld, Dv=%lld)",
                     (long long)a->D, (long long)a->Dv);
+    if (a->dtype == DTATTN_FP32 && (a->D % 4 != 0 || a->Dv % 4 != 0 || a->D > 128 || a->Dv > 128))
+        return fail(DTATTN_ERR_UNSUPPORTED,
+                    "prefill: fp32 head dims must be multiples of 4 up to 128 (D=%lld, Dv=%lld)", (long long)a->D,
+                    (long long)a->Dv);
     // Sequence lengths up to 2^29 keep every causal index expression of the kernels in int32.
     if (a->Sq > (1 << 29) || a->Sk > (1 << 29) || a->B * a->Hq > 0x3fffffff)
         return fail(DTATTN_ERR_UNSUPPORTED, "prefill: sequence length exceeds 2^29");
@@ -551,8 +555,11 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     p.q_xor = sp.q_xor;
     const bool causal = a->causal != 0;
     if (a->dtype == DTATTN_FP32) {
-        p.qk_ch = p.v_ch = (int32_t)(a->D / 4);
-        return prefill_f32(p, (int)a->D, causal, stream);
+        // kernel head dim 64 or 128; smaller real dims (multiples of 4, D and Dv independent) are padded
+        const int Dk = kernel_head_dim(a->D, a->Dv);
+        p.qk_ch = (int32_t)(a->D / 4);
+        p.v_ch = (int32_t)(a->Dv / 4);
+        return prefill_f32(p, Dk, causal, a->D != Dk || a->Dv != Dk, stream);
     }
     // bf16 / fp16: the kernel head dim is the smallest of 64, 128, 256, 512 that holds both real head
     // dims; smaller real dims (multiples of 8, D and Dv independent) run the padded instantiations.

@@ -83,9 +83,12 @@ def test_unsupported_head_dims_raise():
     x = torch.zeros(1, 2, 16, 100, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(ValueError, match="multiples of 8"):
         F.scaled_dot_product_attention(x, x, x)
-    y = torch.zeros(1, 2, 16, 96, dtype=torch.float32, device="cuda")
+    y = torch.zeros(1, 2, 16, 136, dtype=torch.float32, device="cuda")  # fp32 rows: up to 128
     with pytest.raises(ValueError, match="head dim"):
         F.scaled_dot_product_attention(y, y, y)
+    z = torch.zeros(1, 2, 16, 66, dtype=torch.float32, device="cuda")  # fp32 rows: multiples of 4
+    with pytest.raises(ValueError, match="head dim"):
+        F.scaled_dot_product_attention(z, z, z)
 
 
 def _decode(B, Hq, Hkv, Smax, D, lengths, dtype, seed, chunk=0):

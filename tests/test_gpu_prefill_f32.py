@@ -139,3 +139,46 @@ def test_ring_step_fp32():
     rows = slice(idx * C, (idx + 1) * C)
     assert max_abs(host(o), ro[:, :, rows]) <= O_TOL_F32
     assert lse_rel(host(lse), rl[:, :, rows]) <= LSE_TOL_F32
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D,Dv,causal", [
+    (2, 8, 2, 150, 150, 96, 96, True),     # 96 -> kernel 128, GQA 4
+    (1, 4, 4, 130, 257, 80, 80, False),    # 80 -> 128, ragged key tail
+    (1, 2, 2, 100, 100, 32, 32, True),     # 32 -> 64
+    (1, 2, 1, 70, 90, 100, 128, True),     # D 100, Dv 128 at 128
+    (1, 2, 2, 90, 90, 128, 44, False),     # Dv < D at 128
+    (1, 3, 3, 33, 40, 4, 4, False),        # the smallest fp32 head dim (one 16-byte chunk)
+    (1, 2, 2, 65, 64, 60, 36, True),       # both below 64, Sq > Sk
+])
+def test_prefill_f32_padded_head_dims(B, Hq, Hkv, Sq, Sk, D, Dv, causal):
+    # fp32 takes any D and Dv that are multiples of 4 up to 128: the kernel runs at 64 or 128 and
+    # reads the columns past the real dims as zeros; O takes v's last axis
+    # (scaled_dot_product_attention_op.cc:26-29).
+    rng = np.random.default_rng(D * 1000 + Dv)
+    q, k, v = randn(rng, (B, Hq, Sq, D)), randn(rng, (B, Hkv, Sk, D)), randn(rng, (B, Hkv, Sk, Dv))
+    o, lse, ro, rl = _run(q, k, v, causal=causal)
+    assert o.shape == (B, Hq, Sq, Dv)
+    assert max_abs(o, ro) <= O_TOL_F32
+    assert lse_rel(lse, rl) <= LSE_TOL_F32
+
+
+def test_prefill_f32_padded_columns_past_the_row_are_never_read():
+    # head-sliced views of wider fp32 rows whose columns past D / Dv hold NaN, with a mask and causal
+    # offsets: a padded load that touched them would poison the scores or O
+    rng = np.random.default_rng(44)
+    B, H, Sq, Sk, D, Dv = 2, 4, 70, 100, 92, 52
+    q, k, v = randn(rng, (B, H, Sq, D)), randn(rng, (B, H, Sk, D)), randn(rng, (B, H, Sk, Dv))
+    wide = []
+    for x in (q, k, v):
+        w = np.full(x.shape[:-1] + (128,), np.nan, dtype=np.float32)
+        w[..., :x.shape[-1]] = x
+        wide.append(torch.from_numpy(w).cuda()[..., :x.shape[-1]])
+    keep = rng.random((Sq, Sk)) < 0.6
+    keep[:, 0] = True
+    o, lse = _F().scaled_dot_product_attention_with_lse(*wide, is_causal=True, q_offset=30,
+                                                        attn_mask=torch.from_numpy(keep).cuda())
+    torch.cuda.synchronize()
+    ro, rl = orc.sdpa_fwd(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), attn_mask=keep,
+                          is_causal=True, q_offset=30)
+    assert max_abs(host(o), ro) <= O_TOL_F32
+    assert lse_rel(host(lse), rl) <= LSE_TOL_F32

@@ -74,8 +74,10 @@ def _last_error():
     (dict(Hq=6, Hkv=4), 1, "multiple"),
     (dict(D=100, Dv=100), 2, "multiples of 8"),                      # bf16 head dims: multiples of 8
     (dict(D=520, Dv=520), 2, "exceeds 512"),
-    (dict(Dv=64, dtype=3, o_dtype=3), 2, "bf16/fp16 only"),           # D != Dv: 16-bit inputs only
-    (dict(D=96, Dv=96, dtype=3, o_dtype=3), 2, "head dim"),          # fp32: 64 or 128
+    (dict(Dv=64, dtype=2, o_dtype=0, q_descale=0x10000, k_descale=0x10000, v_descale=0x10000), 2,
+     "bf16/fp16/fp32 only"),                                         # D != Dv: not for fp8 codes
+    (dict(D=136, Dv=136, dtype=3, o_dtype=3), 2, "fp32 head dims"),  # fp32: up to 128
+    (dict(D=96, Dv=66, dtype=3, o_dtype=3), 2, "multiples of 4"),    # fp32: multiples of 4
     (dict(D=96, Dv=96, dtype=2, o_dtype=0, q_descale=0x10000, k_descale=0x10000, v_descale=0x10000), 2,
      "head dim"),                                                    # fp8: 64 or 128
     (dict(dtype=5, o_dtype=5), 2, "dtype"),
