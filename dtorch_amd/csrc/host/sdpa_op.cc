@@ -242,12 +242,38 @@ PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::T
     a.dtype = DtypeCode(st);
     a.o_dtype = a.dtype;
     if (fp8) {
-        // per-head e4m3fn quantization and fp8 attention in one call; the K/V codes live in its workspace
+        // per-head e4m3fn quantization and fp8 attention in one call; the K/V codes live in its workspace.
+        // Head dims below 64 or 128 (multiples of 8, D == Dv) are zero-padded to the next of the two and the
+        // output cut back, the rule of the SageAttention package the quantized branch calls
+        // (sage_attn_adapter.cc:28-40 hands it q/k/v as they are): zero columns change no score, no per-head
+        // maximum and no code, and the default scale stays 1/sqrt(real D).
+        const int64_t d = q.D;
+        const int64_t dk = d <= 64 ? 64 : 128;
+        at::Tensor qp, kp, vp, op;
+        if (d == v.D && d % 8 == 0 && d < dk) {
+            qp = at::constant_pad_nd(q.t, {0, dk - d}).reshape({q.B, q.H, q.S, dk});  // contiguous: a view
+            kp = at::constant_pad_nd(k.t, {0, dk - d}).reshape({k.B, k.H, k.S, dk});
+            vp = at::constant_pad_nd(v.t, {0, dk - d}).reshape({v.B, v.H, v.S, dk});
+            op = at::empty({q.B, q.H, q.S, dk}, q_.options());
+            const at::Tensor* src[3] = {&qp, &kp, &vp};
+            int64_t* dst[3] = {a.q_stride, a.k_stride, a.v_stride};
+            for (int i = 0; i < 3; ++i)
+                for (int j = 0; j < 3; ++j) dst[i][j] = src[i]->stride(j);
+            a.q = qp.data_ptr(), a.k = kp.data_ptr(), a.v = vp.data_ptr();
+            a.o = op.data_ptr();
+            for (int j = 0; j < 3; ++j) a.o_stride[j] = op.stride(j);
+            a.D = a.Dv = dk;
+            if (!prm.scale.has_value()) a.scale = (float)(1.0 / std::sqrt((double)d));
+        }
         const size_t ws = dtattn_prefill_fp8_workspace_size(&a);
         at::Tensor wst = at::empty({(int64_t)std::max<size_t>(ws, 1)}, q_.options().dtype(at::kByte));
         a.workspace = wst.data_ptr();
         a.workspace_bytes = ws;
         Check(dtattn_prefill_fp8(&a, stream), "dtattn_prefill_fp8");
+        if (op.defined()) {
+            o.view({q.B, q.H, q.S, d}).copy_(op.narrow(3, 0, d));  // o is freshly allocated, contiguous
+            return {o, lse};
+        }
         if (!ov.t.is_same(o)) o.copy_(ov.t);
         return {o, lse};
     }

@@ -191,9 +191,12 @@ def test_native_fp8_empty_keys_and_errors():
     o, lse = F.scaled_dot_product_attention_with_lse(q, kv, kv, sdpa_option=opt)
     torch.cuda.synchronize()
     assert bool((o == 0).all()) and bool(torch.isneginf(lse).all())
-    x = torch.randn(1, 2, 16, 96, device="cuda", dtype=torch.bfloat16)
+    x = torch.randn(1, 2, 16, 136, device="cuda", dtype=torch.bfloat16)  # above 128
     with pytest.raises(ValueError, match="head dim"):
         F.scaled_dot_product_attention(x, x, x, sdpa_option=opt)
+    x = torch.randn(1, 2, 16, 96, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="head dim"):  # D != Dv
+        F.scaled_dot_product_attention(x, x, x[..., :64], sdpa_option=opt)
     y = torch.randn(1, 2, 16, 128, device="cuda", dtype=torch.float32)
     with pytest.raises(ValueError, match="bf16 or fp16"):
         F.scaled_dot_product_attention(y, y, y, sdpa_option=opt)
@@ -260,3 +263,37 @@ def test_fp8_tail_split(B, Hq, Hkv, Sq, Sk, D, dtype, rows):
     ro, rl = orc.sdpa_fwd(dq, dk, dv, enable_gqa=Hq != Hkv)
     assert max_abs(host(o[:, :, rows]), ro) <= O_TOL_FP8_KERNEL
     assert lse_rel(host(lse[:, :, rows]), rl) <= LSE_TOL
+
+
+@pytest.mark.parametrize("D,causal,dtype,Hq,Hkv", [
+    (96, False, torch.bfloat16, 4, 2),    # -> 128, GQA
+    (80, True, torch.float16, 3, 3),      # -> 128, causal
+    (32, False, torch.bfloat16, 2, 1),    # -> 64
+    (120, True, torch.bfloat16, 2, 2),
+])
+def test_native_fp8_padded_head_dims(D, causal, dtype, Hq, Hkv):
+    # Head dims below 64 / 128 (multiples of 8) run zero-padded, SageAttention's rule: the result equals
+    # exact attention on the per-head dequantized real columns (zero columns change no maximum and no
+    # code), at the kernel bars, with the default scale 1/sqrt(real D); and it is bit-identical to a
+    # call on explicitly zero-padded inputs with that scale.
+    rng = np.random.default_rng(D + Hq)
+    q, k, v = randn(rng, (2, Hq, 300, D)), randn(rng, (2, Hkv, 333, D)), randn(rng, (2, Hkv, 333, D))
+    F = _F()
+    opt = F.SdpaOption(sage_attn_type="native_fp8")
+    tq, tk, tv = (to_dev(x, dtype) for x in (q, k, v))
+    o, lse = F.scaled_dot_product_attention_with_lse(tq, tk, tv, is_causal=causal, enable_gqa=Hq != Hkv,
+                                                     sdpa_option=opt)
+    torch.cuda.synchronize()
+    assert o.shape == (2, Hq, 300, D) and o.dtype == dtype
+    deq = [orc.fp8_dequantize_per_head(*orc.fp8_quantize_per_head(rounded(x, dtype).astype(np.float32)))
+           for x in (q, k, v)]
+    do, dl = orc.sdpa_fwd(*deq, is_causal=causal, enable_gqa=Hq != Hkv)
+    # causal rows with few keys keep e4m3 P's 2^-4 relative error: the causal bar, as in the causal test above
+    assert max_abs(host(o), do) <= (O_TOL_FP8 if causal else O_TOL_FP8_KERNEL)
+    assert lse_rel(host(lse), dl) <= LSE_TOL
+    dk = 64 if D <= 64 else 128
+    pad = [torch.nn.functional.pad(t, (0, dk - D)) for t in (tq, tk, tv)]
+    po, pl = F.scaled_dot_product_attention_with_lse(*pad, is_causal=causal, enable_gqa=Hq != Hkv,
+                                                     scale=1.0 / np.sqrt(D), sdpa_option=opt)
+    torch.cuda.synchronize()
+    assert torch.equal(o, po[..., :D]) and torch.equal(lse, pl)
