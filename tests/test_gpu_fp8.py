@@ -297,3 +297,19 @@ def test_native_fp8_padded_head_dims(D, causal, dtype, Hq, Hkv):
                                                      scale=1.0 / np.sqrt(D), sdpa_option=opt)
     torch.cuda.synchronize()
     assert torch.equal(o, po[..., :D]) and torch.equal(lse, pl)
+
+
+def test_native_fp8_padded_head_dim_rank5_strided_view():
+    # A rank-5 view with a size-1 axis before the heads (batch axes folded by their strides) through the
+    # host's zero-padding: bit-identical to the same call on the contiguous 4-D tensors.
+    g = torch.Generator(device="cuda").manual_seed(5)
+    base = torch.randn(2, 300, 4, 96, generator=g, device="cuda").to(torch.bfloat16)
+    x5 = base.transpose(1, 2).unsqueeze(1)  # [2, 1, 4, 300, 96], strided
+    F = _F()
+    opt = F.SdpaOption(sage_attn_type="native_fp8")
+    o5, l5 = F.scaled_dot_product_attention_with_lse(x5, x5, x5, is_causal=True, sdpa_option=opt)
+    x4 = x5.reshape(2, 4, 300, 96).contiguous()
+    o4, l4 = F.scaled_dot_product_attention_with_lse(x4, x4, x4, is_causal=True, sdpa_option=opt)
+    torch.cuda.synchronize()
+    assert o5.shape == (2, 1, 4, 300, 96) and l5.shape == (2, 1, 4, 300)
+    assert torch.equal(o5.reshape(2, 4, 300, 96), o4) and torch.equal(l5.reshape(2, 4, 300), l4)
