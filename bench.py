@@ -159,6 +159,18 @@ def cpu_decode_baseline(torch, qd, kc, vc, lens_np, dbytes, min_seconds):
     return info
 
 
+def cpu_rate(torch, name, fn, flops, min_seconds, sample, min_reps=3):
+    """One CPU-path timing beside its GPU workload: 1 warm-up, then repetitions for at least `min_seconds`
+    (and at least `min_reps`); TFLOP/s on the same algorithmic FLOPs as the GPU figure."""
+    reps, dt = _timed_reps(fn, min_seconds, min_reps=min_reps)
+    rate = flops * reps / dt
+    threads = torch.get_num_threads()
+    log(f"CPU baseline {name}: {rate / 1e12:.4f} TFLOP/s ({reps} reps, {dt:.1f} s, {threads} threads)")
+    return {"TFLOP/s": round(rate / 1e12, 4), "ms": round(dt / reps * 1e3, 2), "reps": reps,
+            "seconds": round(dt, 1), "threads": threads, "physical_cores": _physical_cores(),
+            "logical_cpus": os.cpu_count(), "sample": sample}
+
+
 def secondary_workloads(torch, F, dev, timer, cpu_info=None, cpu_seconds=0.0):
     extras = {}
     # Cache flush between decode reps: READ 1 GiB (more than the 8 x 4 MB L2 plus the 256 MB MALL), so
@@ -286,6 +298,16 @@ def secondary_workloads(torch, F, dev, timer, cpu_info=None, cpu_seconds=0.0):
                                "frac_hbm": round(mbytes / med_m / PEAK_HBM, 4), "us": round(med_m * 1e6, 1)}
     log(f"ring step 4x4096: blocks {med * 1e3:.3f} ms ({rflops / med / 1e12:.0f} TFLOP/s), merge "
         f"{med_m * 1e6:.1f} us ({mbytes / med_m / 1e9:.0f} GB/s)")
+    if cpu_info is not None:
+        from oracle import dtorch_cpu_path as cpu
+        cq = q4.float().cpu()
+        ck = [x.float().cpu() for x in k4]
+        cv = [x.float().cpu() for x in v4]
+        cpu_info["ring_c4"] = cpu_rate(
+            torch, "C4 ring step", lambda: cpu.ring_step(cq, ck, cv, 3), rflops, cpu_seconds / 2,
+            "libtorch CPU flash attention per block in fp32 on the bf16 values (3 full blocks + the causal "
+            "diagonal, GQA by repeat_kv) and the NumPy LSE merge; whole workload", min_reps=1)
+        del cq, ck, cv
     del q4, k4, v4, blocks
 
     # MMDiT joint attention, bf16 and fp8
@@ -310,6 +332,18 @@ def secondary_workloads(torch, F, dev, timer, cpu_info=None, cpu_seconds=0.0):
                                "note": "end to end: native_fp8 op from bf16 inputs; kernel: attention on codes"}
     log(f"MMDiT 1x24x4608: bf16 {f5 / med / 1e12:.0f} TFLOP/s; fp8 end-to-end {f5 / med8 / 1e12:.0f} TFLOP/s "
         f"({med8 * 1e6:.0f} us), attention kernel on codes {f5 / kern8 / 1e12:.0f} TFLOP/s ({kern8 * 1e6:.0f} us)")
+    if cpu_info is not None:
+        from oracle import dtorch_cpu_path as cpu
+        c5 = [x.float().cpu() for x in (q5, k5, v5)]
+        cpu_info["mmdit_c5a"] = cpu_rate(
+            torch, "C5a MMDiT", lambda: cpu.sdpa(*c5), f5, cpu_seconds / 4,
+            "libtorch CPU SDPA in fp32 on the bf16 values, non-causal, whole workload (B=1, H=24, S=4608, D=128)")
+        deq = [(c.view(torch.float8_e4m3fn).float() * d[..., None, None].float()).cpu() for c, d in
+               ((q8, qd), (k8, kd), (v8, vd))]
+        cpu_info["mmdit_c5b"] = cpu_rate(
+            torch, "C5b MMDiT on dequantized fp8", lambda: cpu.sdpa(*deq), f5, cpu_seconds / 4,
+            "libtorch CPU SDPA in fp32 on the dequantized e4m3fn codes (per-head descales), whole workload")
+        del c5, deq
     del q8, k8, v8
     del q5, k5, v5
 
@@ -324,12 +358,19 @@ def secondary_workloads(torch, F, dev, timer, cpu_info=None, cpu_seconds=0.0):
 
     # the CPU-runnable causal MHA case (B=1, H=8, S=512, D=64) in its own dtype, fp32, and in bf16
     q1, k1, v1 = (torch.randn(1, 8, 512, 64, device=dev, generator=g) for _ in range(3))
+    q1_32, k1_32, v1_32 = q1, k1, v1
     f1 = causal_flops(1, 8, 512, 64)
     med32, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q1, k1, v1, is_causal=True), reps=20)
     q1, k1, v1 = (x.to(torch.bfloat16) for x in (q1, k1, v1))
     med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q1, k1, v1, is_causal=True), reps=20)
     extras["c1_causal_mha_d64"] = {"TFLOP/s_fp32": round(f1 / med32 / 1e12, 2), "us_fp32": round(med32 * 1e6, 1),
                                    "TFLOP/s_bf16": round(f1 / med / 1e12, 2), "us_bf16": round(med * 1e6, 1)}
+    if cpu_info is not None:
+        from oracle import dtorch_cpu_path as cpu
+        c1 = [x.cpu() for x in (q1_32, k1_32, v1_32)]
+        cpu_info["c1_causal_mha_d64"] = cpu_rate(
+            torch, "C1 causal MHA fp32", lambda: cpu.sdpa(*c1, is_causal=True), f1, min(2.0, cpu_seconds / 4),
+            "libtorch CPU SDPA in fp32, causal, B=1 H=8 S=512 D=64 (the reference's own CPU case)")
     del q1, k1, v1
 
     # fp32 prefill on the headline shape (fp32 inputs are computed in fp32 on the fp32 matrix cores)

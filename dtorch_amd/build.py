@@ -118,9 +118,43 @@ def build_c_client(src: str, out: str) -> str:
     return out
 
 
+def build_adapter_check() -> str:
+    """The test module over the DTorch integration adapter (integration/tree/.../dtattn_adapter.cc, the file the
+    integration patch adds to a DTorch tree): the adapter and its pybind wrapper, compiled as the host
+    extension is, in-tree under tests/integration_adapter/."""
+    import torch  # noqa: F401
+    import torch.utils.cpp_extension as ce
+
+    tree = os.path.join(ROOT, "integration", "tree")
+    outdir = os.path.join(ROOT, "tests", "integration_adapter")
+    suffix = sysconfig.get_config_var("EXT_SUFFIX")
+    out = os.path.join(outdir, "_adapter_check" + suffix)
+    incs = ce.include_paths() + [sysconfig.get_paths()["include"], INCLUDE, tree, os.path.join(ROCM, "include")]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cflags = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1",
+              "-DUSE_ROCM=1", "-DTORCH_EXTENSION_NAME=_adapter_check", "-DTORCH_API_INCLUDE_EXTENSION_H"]
+    cflags += [f"-I{i}" for i in incs]
+    srcs = [os.path.join(tree, "dtorch", "external", "dtattn", "dtattn_adapter.cc"), os.path.join(outdir, "bindings.cc")]
+    objs, cmds = [], []
+    for src in srcs:
+        obj = os.path.join(BUILD, "adapter_" + os.path.basename(src) + ".o")
+        objs.append(obj)
+        cmds.append(["g++", *cflags, "-c", src, "-o", obj])
+    with cf.ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+        list(ex.map(_run, cmds))
+    rel = os.path.relpath(PKG, outdir)
+    tmp = out + ".tmp"
+    _run(["g++", "-shared", "-fPIC", *objs, "-o", tmp, f"-L{PKG}", "-ldtattn",
+          *[f"-L{d}" for d in ce.library_paths()], "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+          "-ltorch_python", f"-Wl,-rpath,$ORIGIN/{rel}"])
+    os.replace(tmp, out)
+    return out
+
+
 def build() -> None:
     build_library()
     build_host_extension()
+    build_adapter_check()
 
 
 if __name__ == "__main__":

@@ -66,7 +66,13 @@ public:
 private:
     template <typename T>
     void Get(T& v) {
-        if constexpr (std::is_arithmetic_v<T>) {
+        if constexpr (std::is_same_v<T, bool>) {
+            // one byte that must be 0 or 1: any other value copied into a bool is undefined behaviour
+            uint8_t byte = 0;
+            Get(byte);
+            if (byte > 1) throw std::invalid_argument("dtorch_amd: corrupt bool in param bytes");
+            v = byte != 0;
+        } else if constexpr (std::is_arithmetic_v<T>) {
             if (mBuf.size() - mPos < sizeof(T)) throw std::invalid_argument("dtorch_amd: truncated param bytes");
             std::memcpy(&v, mBuf.data() + mPos, sizeof(T));
             mPos += sizeof(T);

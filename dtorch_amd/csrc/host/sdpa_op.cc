@@ -204,6 +204,27 @@ PrefillResult RunPrefill(const at::Tensor& q_, const at::Tensor& k_, const at::T
     if (fp8 && st != c10::ScalarType::BFloat16 && st != c10::ScalarType::Half)
         Throw("native_fp8 takes bf16 or fp16 inputs");
 
+    // Head dims the kernels do not take directly (16-bit: not a multiple of 8; fp32: not a multiple of 4), as
+    // libtorch takes any (scaled_dot_product_attention_op.cc:107-109 forwards them): q and k are zero-padded
+    // on D and v on Dv to the next multiple, the call runs on the padded tensors with the scale of the real D
+    // (1/sqrt(D) when none is given), and the output is cut back to Dv.  Zero columns add nothing to any score,
+    // and the padded output columns are dropped, so the result is the call on the real dims.
+    {
+        const int64_t step = st == c10::ScalarType::Float ? 4 : 8;
+        const int64_t d = q_.size(-1), dv = v_.size(-1);
+        const int64_t dp = (d + step - 1) / step * step, dvp = (dv + step - 1) / step * step;
+        if ((dp != d || dvp != dv) && d > 0 && dv > 0) {
+            SdpaParam padded = prm;
+            if (!padded.scale.has_value()) padded.scale = 1.0 / std::sqrt((double)d);
+            const at::Tensor qp = dp != d ? at::constant_pad_nd(q_, {0, dp - d}) : q_;
+            const at::Tensor kp = dp != d ? at::constant_pad_nd(k_, {0, dp - d}) : k_;
+            const at::Tensor vp = dvp != dv ? at::constant_pad_nd(v_, {0, dvp - dv}) : v_;
+            PrefillResult r = RunPrefill(qp, kp, vp, padded, qOffset, kOffset, wantLse, mask);
+            if (dvp != dv) r.o = r.o.narrow(-1, 0, dv).contiguous();
+            return r;
+        }
+    }
+
     std::vector<int64_t> oshape = q_.sizes().vec();
     oshape.back() = v_.size(-1);
     at::Tensor o = at::empty(oshape, q_.options());

@@ -3,9 +3,10 @@
 // No counterpart in the reference: its Llama port keeps no cache and recomputes attention over the
 // whole sequence every step (python/dtorch/test/modules/llama.py:126-156).  Token j of sequence b of
 // the new keys/values lands at cache position t = max(lengths[b], 0) + j; positions at or past the
-// capacity (S_max, or max_pages * page_size for a paged cache) are not written.  A second launch on
-// the same stream then advances lengths[b] to min(max(lengths[b], 0) + n_new, capacity), so the
-// copy kernel can read lengths while the update cannot race with it.
+// capacity (S_max, or max_pages * page_size for a paged cache) are not written, and neither are
+// paged positions whose block-table entry is not a page of the pool (below 0 or at least num_pages).
+// A second launch on the same stream then advances lengths[b] to min(max(lengths[b], 0) + n_new,
+// capacity), so the copy kernel can read lengths while the update cannot race with it.
 //
 // HBM-bound copy: one thread per 16-byte chunk of a token row, 16-byte vector loads and stores.
 #include "dtattn_common.hpp"
@@ -46,7 +47,11 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const AppendParams p) {
     const u32x4 vv = ld16(p.v_new + (b * p.vn_b + h * p.vn_h + (int64_t)j * p.vn_s) * p.esz + cb);
     int64_t kbase, vbase;
     if constexpr (PAGED) {
-        const int page = min(max(p.block_table[b * p.bt_s + (t >> p.page_shift)], 0), p.num_pages - 1);
+        // A table entry outside [0, num_pages) names no page of the pool (an unassigned slot, or a corrupt
+        // table): the token is dropped.  Clamping it into the pool, as the decode kernel does for its reads
+        // (whose rows past the length are masked), would overwrite another sequence's cache.
+        const int page = p.block_table[b * p.bt_s + (t >> p.page_shift)];
+        if (page < 0 || page >= p.num_pages) return;
         const int r = t & ((1 << p.page_shift) - 1);
         kbase = page * p.k_b + h * p.k_h + (int64_t)r * p.k_s;
         vbase = page * p.v_b + h * p.v_h + (int64_t)r * p.v_s;

@@ -130,10 +130,12 @@ __global__ void __launch_bounds__(64 * 2 * NRG, 1) prefill_wide_kernel(const Pre
     // tile loads issued before it (5 to 33 waits per tile in the generated code).  Causal D = 512 kernels
     // keep it as well: the spread form measured 28-31% slower there (1x8x2048, D = 512 and 320).
     constexpr bool kSpreadDma = D >= 512 && !MASKED && !CAUSAL;
-    // Resource over tile t's valid rows.  Past the last tile it covers nothing: every load is then out of
-    // range and lands zeros in a buffer no wave reads again.
+    // Resource over tile t's rows below kend (the workgroup's key block, or the causal limit inside it).
+    // Past the block's last tile it covers nothing: every load is then out of range, touches no memory and
+    // lands zeros in a buffer no wave reads again.  Rows of the last tile at or past kend are masked for
+    // every query of the workgroup, so they load as zeros too.
     auto dma_rs = [&](const T* base, int pitch, int64_t stride, int t, int valid_ch, uint32_t* nb) {
-        const int rows = min(BN, p.Sk - t * BN);
+        const int rows = min(BN, kend - t * BN);
         *nb = rows > 0 ? (uint32_t)((rows - 1) * pitch + (PAD ? valid_ch * 16 : D * (int)sizeof(T))) : 0u;
         return make_rsrc(base + (rows > 0 ? (int64_t)t * BN * stride : 0), *nb);
     };

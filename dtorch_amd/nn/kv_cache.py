@@ -101,7 +101,9 @@ class PagedKVCache:
         self.page_size = page_size
         self.scale = scale
         self._free = list(range(num_pages - 1, -1, -1))
-        self._table = np.zeros((batch, max_pages), dtype=np.int32)
+        # unassigned slots hold -1, which names no page: the append kernel drops a token written through one
+        # (a graph replay past a sequence's pages), and decode reads never reach past the length
+        self._table = np.full((batch, max_pages), -1, dtype=np.int32)
         self._pages = np.zeros(batch, dtype=np.int64)  # pages assigned per sequence
         self._host_len = np.zeros(batch, dtype=np.int64)
         self.block_table = torch.from_numpy(self._table).to(device)
@@ -151,9 +153,10 @@ class PagedKVCache:
     def sync_lengths(self) -> np.ndarray:
         """Refresh the host copy of the lengths from the device after HIP-graph replays.
 
-        Replays assign no pages: the block-table slots past a sequence's assigned pages hold page 0, so
-        the caller bounds the replays by the tokens left on the pages already assigned.  Raises if a
-        replay went past them (those tokens were written into page 0).
+        Replays assign no pages: the block-table slots past a sequence's assigned pages hold -1, so the
+        caller bounds the replays by the tokens left on the pages already assigned.  Raises if a replay
+        went past them: those tokens were dropped (no page was written) and the sequence's cache is
+        incomplete.
         """
         dev = self.lengths.to("cpu", torch.int64).numpy().copy()
         if np.any(dev > self._pages * self.page_size):

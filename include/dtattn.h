@@ -168,7 +168,8 @@ int dtattn_decode_splitkv(const dtattn_decode_args* args, void* stream);
  * need more than that (dtattn_decode_workspace_size() with the call's chunk) returns
  * DTATTN_ERR_WORKSPACE.  Nothing is allocated and nothing needs clearing between calls; every call on
  * one device shares the array, so calls that overlap in time on one device (two streams, or two host
- * threads) race and must be ordered by the caller.
+ * threads) race and must be ordered by the caller.  The first call on a device may itself be recorded
+ * under HIP graph capture: the address lookup it makes is not a stream operation.
  */
 #define DTATTN_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int dtattn_decode_splitkv_noalloc(const dtattn_decode_args* args, void* stream);
@@ -238,8 +239,12 @@ typedef struct {
 int dtattn_kv_append(const dtattn_kv_append_args* args, void* stream);
 
 /* The same for a paged cache laid out as dtattn_decode_paged reads it: position t of sequence b is row
- * t % page_size of page block_table[b][t / page_size] (page ids clamped to [0, num_pages)); capacity
- * max_pages * page_size.  The caller assigns the pages of the positions being written beforehand. */
+ * t % page_size of page block_table[b][t / page_size]; capacity max_pages * page_size.  The caller assigns
+ * the pages of the positions being written beforehand.  A token whose table entry is not a page of the pool
+ * (below 0, e.g. an unassigned -1 slot, or at least num_pages) is dropped: nothing is written for it (the
+ * decode reads clamp such ids into the pool instead, since their rows past the length are masked; a write
+ * through a clamped id would land in another sequence's page), and the length advances as for a written
+ * token (ABI version 9). */
 typedef struct {
     const void* k_new;         /* [B, Hkv, n_new, D] (any strides, D stride 1) */
     const void* v_new;

@@ -173,8 +173,10 @@ def kv_append(cache, lengths, new):
 
 def kv_append_paged(pages, block_table, lengths, new):
     """kv_append for a paged cache: position t of sequence b is row t % page_size of page
-    block_table[b, t // page_size] (clamped to the pool) in pages [num_pages, H, page_size, D]; the capacity
-    is max_pages * page_size.  pages and lengths are updated in place."""
+    block_table[b, t // page_size] in pages [num_pages, H, page_size, D]; the capacity is
+    max_pages * page_size.  A token whose table entry is not a page of the pool (below 0 or at least
+    num_pages: an unassigned slot) is dropped, and the length advances as for a written one.  pages and
+    lengths are updated in place."""
     num_pages, _, ps, _ = pages.shape
     cap = block_table.shape[1] * ps
     n_new = new.shape[2]
@@ -184,8 +186,9 @@ def kv_append_paged(pages, block_table, lengths, new):
             t = t0 + j
             if t >= cap:
                 break
-            page = min(max(int(block_table[b, t // ps]), 0), num_pages - 1)
-            pages[page, :, t % ps] = new[b, :, j]
+            page = int(block_table[b, t // ps])
+            if 0 <= page < num_pages:
+                pages[page, :, t % ps] = new[b, :, j]
         lengths[b] = min(t0 + n_new, cap)
 
 

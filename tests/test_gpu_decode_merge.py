@@ -85,10 +85,15 @@ def test_config3_decode_full_size():
     lengths = rng.integers(512, 8192, size=B, endpoint=True).astype(np.int32)
     tk, tv = to_dev(kc), to_dev(vc)
     del kc, vc
+    # rows at or past each sequence's length hold NaN: a kernel that read one would put NaN in O or LSE
+    pad = torch.arange(Smax, device="cuda")[None, :] >= torch.from_numpy(lengths).cuda().long()[:, None]
+    tk.masked_fill_(pad[:, None, :, None], float("nan"))
+    tv.masked_fill_(pad[:, None, :, None], float("nan"))
     F = _F()
     o, lse = F.decode_attention(to_dev(q), tk, tv, torch.from_numpy(lengths).cuda())
     torch.cuda.synchronize()
     o, lse = host(o), host(lse)
+    assert np.isfinite(o).all() and np.isfinite(lse).all()
     kb = tk.float().cpu().numpy()
     vb = tv.float().cpu().numpy()
     ro, rl = orc.decode(rounded(q), kb, vb, lengths)

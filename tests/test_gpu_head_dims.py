@@ -79,16 +79,59 @@ def test_sdpa_op_output_takes_v_head_dim():
 
 
 def test_unsupported_head_dims_raise():
+    # fp32 head dims above 128 have no kernel (the fp32 kernels hold a 128-wide Q row in registers); they raise
+    # rather than fall back
     F = _F()
-    x = torch.zeros(1, 2, 16, 100, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(ValueError, match="multiples of 8"):
-        F.scaled_dot_product_attention(x, x, x)
-    y = torch.zeros(1, 2, 16, 136, dtype=torch.float32, device="cuda")  # fp32 rows: up to 128
+    y = torch.zeros(1, 2, 16, 136, dtype=torch.float32, device="cuda")
     with pytest.raises(ValueError, match="head dim"):
         F.scaled_dot_product_attention(y, y, y)
-    z = torch.zeros(1, 2, 16, 66, dtype=torch.float32, device="cuda")  # fp32 rows: multiples of 4
+    w = torch.zeros(1, 1, 16, 520, dtype=torch.bfloat16, device="cuda")  # 16-bit: up to 512
     with pytest.raises(ValueError, match="head dim"):
-        F.scaled_dot_product_attention(z, z, z)
+        F.scaled_dot_product_attention(w, w, w)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D,Dv,causal,dtype,opt", [
+    (2, 8, 2, 190, 190, 100, 100, True, torch.bfloat16, ""),     # 100 -> 104 (kernel 128), GQA 4
+    (1, 4, 4, 77, 129, 36, 36, False, torch.float16, ""),        # 36 -> 40 (kernel 64)
+    (1, 2, 2, 64, 100, 100, 52, True, torch.bfloat16, ""),       # D and Dv padded apart
+    (1, 2, 1, 70, 90, 300, 300, False, torch.bfloat16, ""),      # 300 -> 304 (wide kernel 512)
+    (1, 4, 2, 66, 66, 66, 66, True, torch.float32, ""),          # fp32: 66 -> 68 (kernel 128)
+    (1, 4, 2, 128, 128, 100, 100, False, torch.bfloat16, "native_fp8"),  # 100 -> 104 -> 128 on the fp8 kernel
+])
+def test_head_dims_off_the_kernel_grid_are_zero_padded(B, Hq, Hkv, Sq, Sk, D, Dv, causal, dtype, opt):
+    # libtorch takes any head dim (scaled_dot_product_attention_op.cc:107-109); the host operator pads q, k on D
+    # and v on Dv with zero columns to the kernels' multiple (8, or 4 for fp32), keeps the scale of the real D and
+    # cuts the output back to Dv
+    rng = np.random.default_rng(D * 100 + Dv + Sk)
+    q, k, v = randn(rng, (B, Hq, Sq, D)), randn(rng, (B, Hkv, Sk, D)), randn(rng, (B, Hkv, Sk, Dv))
+    F = _F()
+    print(f"padded head dims: D={D} Dv={Dv} {dtype} {opt or 'native'}", flush=True)
+    o, lse = F.scaled_dot_product_attention_with_lse(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype),
+                                                     is_causal=causal, enable_gqa=Hq != Hkv,
+                                                     sdpa_option=F.SdpaOption(sage_attn_type=opt or None))
+    torch.cuda.synchronize()
+    assert o.shape == (B, Hq, Sq, Dv) and o.dtype == dtype and o.is_contiguous()
+    if opt == "native_fp8":
+        # against exact attention on the dequantized inputs (per-head e4m3fn of the real columns: the zero
+        # padding changes no absmax), which leaves the kernel's own error, at the fp8 kernel bars
+        deq = [orc.fp8_dequantize_per_head(*orc.fp8_quantize_per_head(rounded(x, dtype).astype(np.float32)))
+               for x in (q, k, v)]
+        ro, rl = orc.sdpa_fwd(*deq, is_causal=causal, enable_gqa=Hq != Hkv, scale=1.0 / np.sqrt(D))
+    else:
+        ro, rl = orc.sdpa_fwd(rounded(q, dtype), rounded(k, dtype), rounded(v, dtype), is_causal=causal,
+                              enable_gqa=Hq != Hkv)
+    if dtype == torch.float32:
+        assert max_abs(host(o), ro) <= 1e-4 and lse_rel(host(lse), rl) <= 1e-5
+    elif opt == "native_fp8":
+        assert max_abs(host(o), ro) <= 3e-2 and lse_rel(host(lse), rl) <= 1e-3
+    else:
+        assert max_abs(host(o), ro) <= O_TOL_BF16 and lse_rel(host(lse), rl) <= LSE_TOL
+    # the explicit scale of the real D gives the same bits as the default
+    o2, _ = F.scaled_dot_product_attention_with_lse(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype),
+                                                    is_causal=causal, enable_gqa=Hq != Hkv, scale=1.0 / np.sqrt(D),
+                                                    sdpa_option=F.SdpaOption(sage_attn_type=opt or None))
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2)
 
 
 def _decode(B, Hq, Hkv, Smax, D, lengths, dtype, seed, chunk=0):

@@ -124,3 +124,71 @@ def test_kv_cache_capacity_is_checked_on_the_host():
     y = torch.zeros(1, 1, 17, 64, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(ValueError, match="pages"):
         paged.append(y, y)
+
+
+def test_kv_append_paged_drops_tokens_without_a_page():
+    # A block-table entry that names no page of the pool (an unassigned -1 slot, or a corrupt id at or past
+    # num_pages) drops the token: no page changes, the length still advances.  A clamp into the pool would
+    # write another sequence's cache.
+    rng = np.random.default_rng(47)
+    B, Hkv, D, ps, max_pages, n = 3, 2, 64, 16, 3, 6
+    P = 7
+    table = np.array([[4, -1, -1], [1, 9, 2], [0, 5, 3]], dtype=np.int32)  # 9 >= num_pages
+    kp, vp = to_dev(randn(rng, (P, Hkv, ps, D))), to_dev(randn(rng, (P, Hkv, ps, D)))
+    lengths = np.array([13, 13, 13], dtype=np.int32)  # tokens 13..18: the last three cross into slot 1
+    kn, vn = to_dev(randn(rng, (B, Hkv, n, D))), to_dev(randn(rng, (B, Hkv, n, D)))
+    before_k, before_v = _bits(kp), _bits(vp)
+    ref_k, ref_v = before_k.copy(), before_v.copy()
+    lk, lv = lengths.astype(np.int64), lengths.astype(np.int64)
+    orc.kv_append_paged(ref_k, table, lk, _bits(kn))
+    orc.kv_append_paged(ref_v, table, lv, _bits(vn))
+    tl = torch.from_numpy(lengths).cuda()
+    _F().kv_cache_append_paged(kp, vp, torch.from_numpy(table).cuda(), tl, kn, vn)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(kp), ref_k) and np.array_equal(_bits(vp), ref_v)
+    assert np.array_equal(tl.cpu().numpy(), np.full(B, 19))
+    # only rows 13..15 of the pages in slot 0 changed; page 6 (never named) and the pages of slot 1 of
+    # sequences 1 and 2 (their tokens 16..18 went to pages 9 -> dropped, and 5) are checked explicitly
+    changed = np.nonzero(np.any(_bits(kp) != before_k, axis=(1, 2, 3)))[0].tolist()
+    assert changed == [0, 1, 4, 5]
+    assert np.array_equal(_bits(kp)[6], before_k[6])
+
+
+def test_paged_graph_replays_past_assigned_pages_write_nothing_else():
+    # A decode step captured in a HIP graph and replayed past a sequence's assigned pages: the tokens past
+    # them meet table slots of -1 and are dropped, every page that no sequence owns stays bit-identical, the
+    # owned pages equal the oracle's append, and sync_lengths() reports the overrun.
+    from dtorch_amd.nn.kv_cache import PagedKVCache
+    rng = np.random.default_rng(48)
+    B, Hq, Hkv, D, ps, L0, replays = 2, 8, 2, 64, 16, 20, 15
+    cache = PagedKVCache(B, Hkv, num_pages=8, page_size=ps, max_pages=4, head_dim=D)
+    cache.k.copy_(to_dev(randn(rng, tuple(cache.k.shape))))
+    cache.v.copy_(to_dev(randn(rng, tuple(cache.v.shape))))
+    q, k, v = (to_dev(randn(rng, (B, h, L0, D))) for h in (Hq, Hkv, Hkv))
+    cache.prefill(q, k, v)  # two pages per sequence; slots 2 and 3 stay -1
+    torch.cuda.synchronize()
+    table = cache.block_table.cpu().numpy()
+    assert np.array_equal(table[:, 2:], np.full((B, 2), -1))
+    owned = set(table[table >= 0].tolist())
+    before_k, before_v = _bits(cache.k), _bits(cache.v)
+    sq, sk, sv = (to_dev(randn(rng, (B, h, 1, D))) for h in (Hq, Hkv, Hkv))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cache.decode(sq, sk, sv)
+    torch.cuda.synchronize()
+    ref_k, ref_v = before_k.copy(), before_v.copy()
+    lk = np.full(B, L0, dtype=np.int64)
+    lv = lk.copy()
+    for _ in range(replays):  # lengths 20 -> 35; positions 32..34 fall in slot 2
+        graph.replay()
+        torch.cuda.synchronize()  # eager work between replays
+        orc.kv_append_paged(ref_k, table, lk, _bits(sk))
+        orc.kv_append_paged(ref_v, table, lv, _bits(sv))
+    assert np.array_equal(_bits(cache.k), ref_k) and np.array_equal(_bits(cache.v), ref_v)
+    for pg in range(cache.k.shape[0]):
+        if pg not in owned:
+            assert np.array_equal(_bits(cache.k)[pg], before_k[pg]), pg
+            assert np.array_equal(_bits(cache.v)[pg], before_v[pg]), pg
+    assert np.array_equal(cache.lengths.cpu().numpy(), np.full(B, L0 + replays))
+    with pytest.raises(RuntimeError, match="past the assigned pages"):
+        cache.sync_lengths()

@@ -349,6 +349,12 @@ def test_every_param_type_round_trips_in_field_order():
         host.SdpaParam.from_bytes(lp.to_bytes())
     with pytest.raises(ValueError, match="truncated"):
         host.SdpaWithLseParam.from_bytes(base.to_bytes())
+    # a bool byte other than 0 or 1 (isCausal, then enableGqa) is rejected rather than copied into a bool
+    for pos in (0, 1 + 1 + 8):
+        bad = bytearray(want)
+        bad[pos] = 2
+        with pytest.raises(ValueError, match="corrupt bool"):
+            host.SdpaParam.from_bytes(bytes(bad))
     # the operators keep their params
     assert host.SdpaWithLseOp(lp).lse_param.q_offset == 4096
     assert host.SdpaDecodeOp(host.SdpaDecodeParam(None, 128)).param.chunk == 128

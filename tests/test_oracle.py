@@ -45,6 +45,24 @@ def test_golden_decode(golden):
     assert np.max(np.abs(o - g["o"])) < 2e-5
 
 
+def test_cpu_path_decode_matches_golden_and_oracle(golden):
+    # DTorch's CPU path for decode (a per-sequence libtorch call over the true length, Lq = 1, GQA) against
+    # the committed fixture and the fp64 oracle; with the padding rows poisoned with NaN, so that a loop
+    # reading past a sequence's length would fail.
+    g = {k.split("/", 1)[1]: golden[k] for k in golden.files if k.startswith("decode/")}
+    kc, vc = g["k"].copy(), g["v"].copy()
+    for b, L in enumerate(g["lengths"]):
+        kc[b, :, int(L):] = np.nan
+        vc[b, :, int(L):] = np.nan
+    o = cpu.decode(_t(g["q"]), _t(kc), _t(vc), [int(x) for x in g["lengths"]]).double().numpy()
+    assert np.max(np.abs(o - g["o"])) < 2e-6
+    ro, _ = orc.decode(g["q"], g["k"], g["v"], g["lengths"])
+    assert np.max(np.abs(o - ro)) < 2e-5
+    # a planted mistake: attending over the padded capacity instead of the true lengths
+    wrong = cpu.decode(_t(g["q"]), _t(g["k"]), _t(g["v"]), [g["k"].shape[2]] * len(g["lengths"])).double().numpy()
+    assert np.max(np.abs(wrong - g["o"])) > 1e-2
+
+
 def test_golden_fp8(golden):
     g = {k.split("/", 1)[1]: golden[k] for k in golden.files if k.startswith("fp8/")}
     codes, desc = orc.fp8_quantize_per_head(g["x"])
@@ -368,6 +386,35 @@ def test_kv_append_paged_matches_contiguous():
     assert np.array_equal(lp, lc)
     assert np.array_equal(orc.gather_pages(pages, table, lp, max_len=max_pages * ps), np.where(
         np.arange(max_pages * ps)[None, None, :, None] < lc[:, None, None, None], contig, 0.0))
+
+
+def test_kv_append_paged_drops_tokens_without_a_page():
+    # The drop rule pinned against the contiguous append: a token whose slot names no page of the pool (-1,
+    # or an id at or past num_pages) writes nothing, and the length advances as for a written token.  Pages
+    # written through valid slots equal the contiguous cache's rows; no other page changes (a clamp into
+    # the pool would overwrite page 0 or the last page, both of which hold other data here).
+    rng = np.random.default_rng(34)
+    B, H, D, ps, max_pages = 2, 1, 4, 16, 3
+    P = 5
+    table = np.array([[3, -1, 1], [2, 7, -5]], dtype=np.int32)
+    pages = rng.standard_normal((P, H, ps, D))
+    before = pages.copy()
+    contig = np.zeros((B, H, max_pages * ps, D))
+    lp = np.array([10, 12], dtype=np.int64)
+    lc = lp.copy()
+    new = rng.standard_normal((B, H, 30, D))
+    orc.kv_append_paged(pages, table, lp, new)
+    orc.kv_append(contig, lc, new)
+    assert np.array_equal(lp, lc) and np.array_equal(lp, [40, 42])
+    for b in range(B):
+        for slot in range(max_pages):
+            pg = int(table[b, slot])
+            rows = range(slot * ps, (slot + 1) * ps)
+            if 0 <= pg < P:
+                for t in rows:
+                    want = contig[b, :, t] if lc[b] - 30 <= t < lc[b] else before[pg, :, t % ps]
+                    assert np.array_equal(pages[pg, :, t % ps], want), (b, slot, t)
+    assert np.array_equal(pages[0], before[0]) and np.array_equal(pages[4], before[4])
 
 
 def test_masks_match_libtorch():

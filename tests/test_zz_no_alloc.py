@@ -115,3 +115,77 @@ def test_noalloc_decode_rejects_calls_beyond_the_scratch():
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     assert lib.dtattn_decode_splitkv_noalloc(ctypes.byref(a), stream) == 3  # DTATTN_ERR_WORKSPACE
     assert b"scratch" in lib.dtattn_last_error()
+
+
+_FIRST_CALL_CAPTURED = r'''
+import ctypes, os, sys
+sys.path.insert(0, os.environ["DTATTN_REPO"])
+import torch
+import tests.test_zz_no_alloc as T
+lib = T._lib()
+q, k, v, lengths = T._case(4, 8, 2, 1000, 128, torch.bfloat16, 7)
+o_na, l_na = torch.empty_like(q), torch.empty(4, 8, device="cuda")
+a = T._args(q, k, v, lengths, o_na, l_na, T.BF16)
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):  # the process's first noalloc call: the scratch lookup runs under capture
+    st = lib.dtattn_decode_splitkv_noalloc(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+assert st == 0, lib.dtattn_last_error()
+for _ in range(3):
+    o_na.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+o_ref, l_ref = torch.empty_like(q), torch.empty(4, 8, device="cuda")
+ws = torch.empty(lib.dtattn_decode_workspace_size(4, 8, 1000, 128, 0), dtype=torch.uint8, device="cuda")
+r = T._args(q, k, v, lengths, o_ref, l_ref, T.BF16, 0, ws)
+assert lib.dtattn_decode_splitkv(ctypes.byref(r), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
+torch.cuda.synchronize()
+assert torch.equal(o_na, o_ref) and torch.equal(l_na, l_ref)
+print("first call captured: replays equal the allocating entry point")
+'''
+
+
+def test_noalloc_first_call_of_a_process_under_graph_capture():
+    # The per-device scratch address is looked up on a device's first call; here that call is recorded into
+    # a HIP graph in a fresh process (so no earlier test has made the lookup), and its replays must equal
+    # the allocating entry point.
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, DTATTN_REPO=root)
+    print("noalloc decode: first call of a fresh process under graph capture (subprocess)", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED], cwd=root, env=env, capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "replays equal the allocating entry point" in r.stdout
+
+
+def test_noalloc_graph_replay_after_an_eager_call_on_another_shape():
+    # One scratch array per device: a captured call replayed after an eager noalloc call of another shape
+    # (which left its own partials in the scratch) must still equal the allocating entry point, and so must
+    # that eager call.  Calls on one stream are ordered, so they share the scratch safely.
+    lib = _lib()
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    qa, ka, va, la = _case(16, 32, 8, 3000, 128, torch.bfloat16, 21)
+    qb, kb, vb, lb = _case(5, 8, 8, 777, 64, torch.float16, 22)
+    oa, sa = torch.empty_like(qa), torch.empty(16, 32, device="cuda")
+    ob, sb = torch.empty_like(qb), torch.empty(5, 8, device="cuda")
+    a = _args(qa, ka, va, la, oa, sa, BF16)
+    b = _args(qb, kb, vb, lb, ob, sb, FP16)
+    assert lib.dtattn_decode_splitkv_noalloc(ctypes.byref(a), stream()) == 0  # eager warm-up of shape A
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert lib.dtattn_decode_splitkv_noalloc(ctypes.byref(a), stream()) == 0
+    torch.cuda.synchronize()
+    ref_a = _both(lib, 16, 32, 8, 3000, 128, torch.bfloat16, BF16, 0, 21)
+    ref_b = _both(lib, 5, 8, 8, 777, 64, torch.float16, FP16, 0, 22)
+    for _ in range(2):
+        oa.zero_()
+        ob.zero_()
+        assert lib.dtattn_decode_splitkv_noalloc(ctypes.byref(b), stream()) == 0  # eager, shape B
+        graph.replay()                                                         # shape A from the graph
+        torch.cuda.synchronize()
+        assert torch.equal(ob, ref_b[0]) and torch.equal(sb, ref_b[1])
+        assert torch.equal(oa, ref_a[0]) and torch.equal(sa, ref_a[1])
