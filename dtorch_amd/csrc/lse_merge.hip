@@ -3,10 +3,10 @@
 // No counterpart in the reference: its ring context parallelism all-gathers K/V and runs one SDPA
 // (python/dtorch/nn/scaled_dot_product_attention_with_cp.py:87-101).  Closed form, per query row:
 //   m = max_b LSE_b,  LSE = m + log sum_b exp(LSE_b - m),  O = sum_b exp(LSE_b - LSE) O_b.
-// HBM-bound: one thread per 16-byte output chunk (8 elements); each thread reads the n LSE values of
-// its row (shared by the D/8 threads of the row through L1) and n input chunks, and writes one chunk.
-// A workgroup covers 256 consecutive chunks of one (batch, head) slab, so the only divisions are
-// per workgroup and scalar; a thread's row and chunk come from shifts.
+// HBM-bound: each thread merges one 16-byte output chunk (8 elements), or two for n = 2 and n = 4; per chunk
+// it reads the n LSE values of its row (shared by the D/8 threads of the row through L1) and n input chunks,
+// and writes one chunk.  A workgroup covers 256 (or 512) consecutive chunks of one (batch, head) slab, so
+// the only divisions are per workgroup and scalar; a thread's row and chunk come from shifts.
 #include "dtattn_common.hpp"
 
 namespace dtattn {
@@ -22,88 +22,122 @@ struct MergeParams {
     int64_t l_b, l_h;
     int64_t slabs;  // B * H
     int32_t H, S, n;
-    int32_t wg_per_slab;  // ceil(S * D / 8 / 256)
+    int32_t wg_per_slab;  // ceil(S * D / 8 / (256 * chunks per thread))
     int32_t cpr;          // 16-byte chunks per row (D / 8); read by the generic (D = 0) instantiation
 };
 
-// Block outputs are read exactly once: non-temporal loads (load_chunk<TI, true>).  The merged output
-// is written with non-temporal stores too: measured +9.5% at 4 blocks of [1, 32, 4096, 128] bf16
-// (4.72 -> 5.16 TB/s), bit-identical.
+// Block outputs are read exactly once: non-temporal loads (load_chunk<TI, true>).  The merged output is
+// written through to memory (cache policy sc0 sc1, vector stores): at 4 blocks of [1, 32, 4096, 128] bf16
+// from HBM that measured 33.7 -> 31.3 us per launch against non-temporal stores, and 34.4 with plain ones.
+// The compiler has no intrinsic for this policy on a 16-byte global store and does not see into the asm,
+// so the asm pays the hazard it would otherwise insert: a VALU write to the data VGPRs of a store wider
+// than 8 bytes needs two wait states after it on gfx950 (s_nop 1).  Nothing after the store waits on it.
+__device__ __forceinline__ void st16_wt(void* p, u32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
+}
 
 template <typename TO>
-__device__ __forceinline__ void store8(TO* p, const float* in);
-template <>
-__device__ __forceinline__ void store8<bf16_t>(bf16_t* p, const float* in) {
-    __builtin_nontemporal_store(pack8<bf16_t>(in), reinterpret_cast<u32x4*>(p));
+__device__ __forceinline__ void store8(TO* p, const float* in) {
+    if constexpr (sizeof(TO) == 4) {
+        st16_wt(p, __builtin_bit_cast(u32x4, f32x4{in[0], in[1], in[2], in[3]}));
+        st16_wt(p + 4, __builtin_bit_cast(u32x4, f32x4{in[4], in[5], in[6], in[7]}));
+    } else {
+        st16_wt(p, pack8<TO>(in));
+    }
 }
-template <>
-__device__ __forceinline__ void store8<f16_t>(f16_t* p, const float* in) {
-    __builtin_nontemporal_store(pack8<f16_t>(in), reinterpret_cast<u32x4*>(p));
-}
-template <>
-__device__ __forceinline__ void store8<float>(float* p, const float* in) {
-    __builtin_nontemporal_store(f32x4{in[0], in[1], in[2], in[3]}, reinterpret_cast<f32x4*>(p));
-    __builtin_nontemporal_store(f32x4{in[4], in[5], in[6], in[7]}, reinterpret_cast<f32x4*>(p + 4));
+
+// Chunks per thread: two for n = 2 and n = 4 (every load of both in one round trip: 33.7 -> 30.3 us at
+// 4 blocks of [1, 32, 4096, 128] bf16, with half the workgroups), one for the generic n.
+template <int NB>
+constexpr int merge_cpt() {
+    return NB > 0 ? 2 : 1;
 }
 
 // D = 0: any head dim that is a multiple of 8, with the row split computed at run time.
 template <typename TI, typename TO, int D, int NB>
 __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeParams p) {
+    constexpr int CPT = merge_cpt<NB>();
     const int64_t bh = blockIdx.x / p.wg_per_slab;  // wave-uniform
-    const int idx = (int)(blockIdx.x - bh * p.wg_per_slab) * 256 + (int)threadIdx.x;
+    const int idx0 = (int)(blockIdx.x - bh * p.wg_per_slab) * (256 * CPT) + (int)threadIdx.x;
     const int cpr = D > 0 ? D / 8 : p.cpr;  // chunks per row (a power of two when D > 0)
-    const int s = idx / cpr, c = idx - s * cpr;
-    if (s >= p.S) return;
+    int s[CPT], c[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        s[k] = (idx0 + k * 256) / cpr;
+        c[k] = idx0 + k * 256 - s[k] * cpr;
+    }
+    if (s[0] >= p.S) return;
     const int h = (int)(bh % p.H);
     const int64_t b = bh / p.H;
     const int n = NB > 0 ? NB : p.n;
-    const int64_t lse_off = b * p.bl_b + h * p.bl_h + s;
-    const int64_t in_off = b * p.bo_b + h * p.bo_h + (int64_t)s * p.bo_s + c * 8;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int64_t lse_b = b * p.bl_b + h * p.bl_h;
+    const int64_t in_b = b * p.bo_b + h * p.bo_h;
+    const int64_t out_b = b * p.o_b + h * p.o_h;
     // A block with weight 0 (LSE = -inf) adds nothing, whatever its O holds (NaN included).
-    auto add = [&](const Chunk<TI>& raw, float w) {
+    auto add = [](float* acc, const Chunk<TI>& raw, float w) {
         float x[8];
         unpack_chunk<TI>(raw, x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = w != 0.f ? __builtin_fmaf(w, x[e], acc[e]) : acc[e];
     };
-    float m = kNegInf, sum = 0.f, mb;
+    auto finish = [&](int k, const float* acc, float mb, float sum) {
+        store8<TO>(reinterpret_cast<TO*>(p.o) + out_b + (int64_t)s[k] * p.o_s + c[k] * 8, acc);
+        if (p.lse != nullptr && c[k] == 0)
+            p.lse[b * p.l_b + h * p.l_h + s[k]] = sum > 0.f ? mb + __logf(sum) : kNegInf;
+    };
     if constexpr (NB > 0) {
-        // every LSE and O load of the thread in one memory round trip
-        float l[NB];
-        Chunk<TI> raw[NB];
+        // Every LSE and O load of the thread's chunks in one memory round trip.  A second chunk past the
+        // slab's last row loads that row again (unconditional loads keep the waits counted) and stores nothing.
+        const bool second = s[CPT - 1] < p.S;
+        float l[CPT][NB];
+        Chunk<TI> raw[CPT][NB];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            l[i] = p.lse_blocks[i][lse_off];
-            raw[i] = load_chunk<TI, true>(reinterpret_cast<const TI*>(p.o_blocks[i]) + in_off);
+        for (int k = 0; k < CPT; ++k) {
+            const int sl = min(s[k], p.S - 1);
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                l[k][i] = p.lse_blocks[i][lse_b + sl];
+                raw[k][i] = load_chunk<TI, true>(reinterpret_cast<const TI*>(p.o_blocks[i]) + in_b +
+                                                 (int64_t)sl * p.bo_s + c[k] * 8);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);  // keeps the scheduler from issuing the later loads after waits
 #pragma unroll
-        for (int i = 0; i < NB; ++i) m = fmaxf(m, l[i]);
-        mb = m == kNegInf ? 0.f : m;
+        for (int k = 0; k < CPT; ++k) {
+            if (k > 0 && !second) break;
+            float m = kNegInf, sum = 0.f;
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            l[i] = __expf(l[i] - mb);
-            sum += l[i];
+            for (int i = 0; i < NB; ++i) m = fmaxf(m, l[k][i]);
+            const float mb = m == kNegInf ? 0.f : m;
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                l[k][i] = __expf(l[k][i] - mb);
+                sum += l[k][i];
+            }
+            const float inv = sum > 0.f ? 1.f / sum : 0.f;
+            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < NB; ++i) add(acc, raw[k][i], l[k][i] * inv);
+            finish(k, acc, mb, sum);
         }
-        const float inv = sum > 0.f ? 1.f / sum : 0.f;
-#pragma unroll
-        for (int i = 0; i < NB; ++i) add(raw[i], l[i] * inv);
     } else {
         // the n LSE values first, then the O chunks in batches of four loads in flight together
+        const int64_t in_off = in_b + (int64_t)s[0] * p.bo_s + c[0] * 8;
         float l[DTATTN_MAX_MERGE_BLOCKS];
 #pragma unroll
-        for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) l[i] = i < n ? p.lse_blocks[i][lse_off] : kNegInf;
+        for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) l[i] = i < n ? p.lse_blocks[i][lse_b + s[0]] : kNegInf;
         __builtin_amdgcn_sched_barrier(0);
+        float m = kNegInf, sum = 0.f;
 #pragma unroll
         for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) m = fmaxf(m, l[i]);
-        mb = m == kNegInf ? 0.f : m;
+        const float mb = m == kNegInf ? 0.f : m;
 #pragma unroll
         for (int i = 0; i < DTATTN_MAX_MERGE_BLOCKS; ++i) {
             l[i] = __expf(l[i] - mb);  // blocks past n have LSE -inf: weight 0
             sum += l[i];
         }
         const float inv = sum > 0.f ? 1.f / sum : 0.f;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i0 = 0; i0 < DTATTN_MAX_MERGE_BLOCKS; i0 += 4) {
             if (i0 >= n) break;
@@ -113,17 +147,17 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeParams p) {
                 if (i0 + j < n) raw[j] = load_chunk<TI, true>(reinterpret_cast<const TI*>(p.o_blocks[i0 + j]) + in_off);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) add(raw[j], l[i0 + j] * inv);
+            for (int j = 0; j < 4; ++j) add(acc, raw[j], l[i0 + j] * inv);
         }
+        finish(0, acc, mb, sum);
     }
-    store8<TO>(reinterpret_cast<TO*>(p.o) + b * p.o_b + h * p.o_h + (int64_t)s * p.o_s + c * 8, acc);
-    if (p.lse != nullptr && c == 0) p.lse[b * p.l_b + h * p.l_h + s] = sum > 0.f ? mb + __logf(sum) : kNegInf;
 }
 
 template <typename TI, typename TO, int D>
 static int launch_merge(const MergeParams& p, hipStream_t stream) {
     MergeParams q = p;
-    q.wg_per_slab = (int32_t)(((int64_t)p.S * p.cpr + 255) / 256);
+    const int64_t per_wg = 256 * (p.n == 2 || p.n == 4 ? merge_cpt<2>() : merge_cpt<0>());
+    q.wg_per_slab = (int32_t)(((int64_t)p.S * p.cpr + per_wg - 1) / per_wg);
     const int64_t blocks = p.slabs * q.wg_per_slab;
     if (blocks == 0) return DTATTN_OK;
     if (blocks > 0x7fffffff) return fail(DTATTN_ERR_UNSUPPORTED, "merge: grid too large");
@@ -172,8 +206,8 @@ extern "C" int dtattn_lse_merge(const dtattn_merge_args* a, void* stream_) {
     if (a->D % 8 != 0 || a->D > 4096)
         return fail(DTATTN_ERR_UNSUPPORTED, "merge: head dim %lld must be a multiple of 8 up to 4096", (long long)a->D);
     if (a->B == 0 || a->H == 0 || a->S == 0) return DTATTN_OK;
-    // chunk indices within one (batch, head) slab are int32
-    if (a->S * (a->D / 8) >= ((int64_t)1 << 31) || a->H > 0x7fffffff)
+    // chunk indices within one (batch, head) slab, rounded up to whole workgroups, are int32
+    if (a->S * (a->D / 8) >= ((int64_t)1 << 31) - 512 || a->H > 0x7fffffff)
         return fail(DTATTN_ERR_UNSUPPORTED, "merge: sizes too large");
     if (a->o == nullptr) return fail(DTATTN_ERR_INVALID_ARGUMENT, "merge: null output");
     const int in_esz = a->block_dtype == DTATTN_FP32 ? 4 : 2;
