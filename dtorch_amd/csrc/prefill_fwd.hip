@@ -224,12 +224,16 @@ __global__ void __launch_bounds__(256, 2) prefill_fwd_kernel(const PrefillParams
         const float mcand = fmaxf(mrow, mx * p.c);
         if (__any(mcand - mrow > kRescaleThreshold)) {  // wave-uniform
             const float alpha = fast_exp2(mrow - (mcand == kNegInf ? 0.f : mcand));
+            // A lane whose max is still -inf has seen no visible key: its O and l are exactly 0.  When
+            // that holds for the whole wave (its first tile) the multiply is skipped.
+            if (!__all(mrow == kNegInf)) {
+                lrow *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+            }
             mrow = mcand;
-            lrow *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
         }
         // Wave priority: raised over the exponential/PV block of the non-causal kernel only.  Measured
         // A/B on one MI355X: MMDiT 1x24x4608 +4.5% against raising it over both blocks; the causal
