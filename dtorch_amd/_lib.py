@@ -50,7 +50,7 @@ def cabi() -> ctypes.CDLL:
 # ctypes mirrors of the C ABI's argument structs (include/dtattn.h), for callers that drive the library
 # directly: the codes entry point of the fp8 path, the allocation-free decode, tests of the ABI itself.
 class PrefillArgs(ctypes.Structure):
-    """dtattn_prefill_args (ABI version 9, same layout as 8); `scale` starts as NaN, the ABI's "1/sqrt(D)"."""
+    """dtattn_prefill_args (ABI version 10, same layout as 8); `scale` starts as NaN, the ABI's "1/sqrt(D)"."""
     _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("o", ctypes.c_void_p),
                 ("lse", ctypes.c_void_p),
                 ("B", ctypes.c_int64), ("Hq", ctypes.c_int64), ("Hkv", ctypes.c_int64), ("Sq", ctypes.c_int64),
@@ -70,7 +70,7 @@ class PrefillArgs(ctypes.Structure):
 
 
 class DecodeArgs(ctypes.Structure):
-    """dtattn_decode_args (ABI version 9, same layout as 8); `scale` starts as NaN, the ABI's "1/sqrt(D)"."""
+    """dtattn_decode_args (ABI version 10, same layout as 8); `scale` starts as NaN, the ABI's "1/sqrt(D)"."""
     _fields_ = [("q", ctypes.c_void_p), ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
                 ("lengths", ctypes.c_void_p), ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p),
                 ("B", ctypes.c_int64), ("Hq", ctypes.c_int64), ("Hkv", ctypes.c_int64), ("S_max", ctypes.c_int64),

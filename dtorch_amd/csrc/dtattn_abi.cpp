@@ -40,7 +40,10 @@ int check_launch(const char* what) {
 // |scale| are those of a negative scale; with q zeroed every logit is 0 (+ mask), as at scale 0.
 int plan_scale(float scale, int64_t D, uint32_t sign_bits, ScalePlan* out) {
     if (std::isnan(scale)) {
-        *out = ScalePlan{1.0f / sqrtf((float)D), 0xffffffffu, 0u};
+        // 1/sqrt(D) in double, rounded once to float: libtorch's default scale, and the value a caller gets
+        // by passing 1/sqrt(D) explicitly (an fp32 quotient of an fp32 root differs in the last bit for some
+        // D, e.g. 96 and 300)
+        *out = ScalePlan{(float)(1.0 / std::sqrt((double)D)), 0xffffffffu, 0u};
         return DTATTN_OK;
     }
     if (std::isinf(scale)) return fail(DTATTN_ERR_INVALID_ARGUMENT, "scale must be finite (NaN selects 1/sqrt(D))");

@@ -461,9 +461,9 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     if (sixteen_bit && (a->D % 8 != 0 || a->Dv % 8 != 0))
         return fail(DTATTN_ERR_UNSUPPORTED, "prefill: head dims must be multiples of 8 (D=%lld, Dv=%lld)",
                     (long long)a->D, (long long)a->Dv);
-    if (a->dtype == DTATTN_FP32 && (a->D % 4 != 0 || a->Dv % 4 != 0 || a->D > 128 || a->Dv > 128))
+    if (a->dtype == DTATTN_FP32 && (a->D % 4 != 0 || a->Dv % 4 != 0 || a->D > 512 || a->Dv > 512))
         return fail(DTATTN_ERR_UNSUPPORTED,
-                    "prefill: fp32 head dims must be multiples of 4 up to 128 (D=%lld, Dv=%lld)", (long long)a->D,
+                    "prefill: fp32 head dims must be multiples of 4 up to 512 (D=%lld, Dv=%lld)", (long long)a->D,
                     (long long)a->Dv);
     // Sequence lengths up to 2^29 keep every causal index expression of the kernels in int32.
     if (a->Sq > (1 << 29) || a->Sk > (1 << 29) || a->B * a->Hq > 0x3fffffff)
@@ -559,7 +559,8 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
     p.q_xor = sp.q_xor;
     const bool causal = a->causal != 0;
     if (a->dtype == DTATTN_FP32) {
-        // kernel head dim 64 or 128; smaller real dims (multiples of 4, D and Dv independent) are padded
+        // kernel head dim 64, 128, 256 or 512 (the last two on the wide fp32 kernel); smaller real dims
+        // (multiples of 4, D and Dv independent) are padded
         const int Dk = kernel_head_dim(a->D, a->Dv);
         p.qk_ch = (int32_t)(a->D / 4);
         p.v_ch = (int32_t)(a->Dv / 4);

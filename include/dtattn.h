@@ -22,9 +22,10 @@
 extern "C" {
 #endif
 
-#define DTATTN_ABI_VERSION 9
+#define DTATTN_ABI_VERSION 10
 
-/* Softmax scale fields (ABI version 8): NaN selects 1/sqrt(D); any finite value is used as given,
+/* Softmax scale fields (ABI version 8): NaN selects 1/sqrt(D) (computed in double and rounded once to
+ * float, as libtorch computes its default, from ABI version 10); any finite value is used as given,
  * zero and negative included, as torch::scaled_dot_product_attention takes SdpaParam's scale
  * (scaled_dot_product_attention_op.cc:107-109); +-inf is rejected.  Up to version 7 a scale <= 0
  * selected 1/sqrt(D). */
@@ -61,8 +62,8 @@ typedef enum {
  * Head dims: BF16/FP16 take any D and Dv that are multiples of 8 up to 512, independently (the output
  * takes v's last axis, as scaled_dot_product_attention_op.cc:26-29 does); the kernels run at 64, 128,
  * 256 or 512 and read the columns past the real dims as zeros (ABI version 6).  FP32 takes any D and
- * Dv that are multiples of 4 up to 128, independently, the same way at 64 or 128 (ABI version 9).  FP8
- * takes D == Dv in {64, 128}.
+ * Dv that are multiples of 4 up to 512, independently, the same way at 64, 128, 256 or 512 (up to 128
+ * from ABI version 9, up to 512 from version 10).  FP8 takes D == Dv in {64, 128}.
  */
 typedef struct {
     const void* q; /* [B, Hq, Sq, D] */

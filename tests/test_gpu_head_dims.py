@@ -79,10 +79,9 @@ def test_sdpa_op_output_takes_v_head_dim():
 
 
 def test_unsupported_head_dims_raise():
-    # fp32 head dims above 128 have no kernel (the fp32 kernels hold a 128-wide Q row in registers); they raise
-    # rather than fall back
+    # head dims above 512 have no kernel in any dtype; they raise rather than fall back
     F = _F()
-    y = torch.zeros(1, 2, 16, 136, dtype=torch.float32, device="cuda")
+    y = torch.zeros(1, 2, 16, 520, dtype=torch.float32, device="cuda")
     with pytest.raises(ValueError, match="head dim"):
         F.scaled_dot_product_attention(y, y, y)
     w = torch.zeros(1, 1, 16, 520, dtype=torch.bfloat16, device="cuda")  # 16-bit: up to 512
@@ -96,6 +95,8 @@ def test_unsupported_head_dims_raise():
     (1, 2, 2, 64, 100, 100, 52, True, torch.bfloat16, ""),       # D and Dv padded apart
     (1, 2, 1, 70, 90, 300, 300, False, torch.bfloat16, ""),      # 300 -> 304 (wide kernel 512)
     (1, 4, 2, 66, 66, 66, 66, True, torch.float32, ""),          # fp32: 66 -> 68 (kernel 128)
+    (1, 2, 1, 70, 90, 300, 300, False, torch.float32, ""),       # fp32: 300 (wide fp32 kernel 512)
+    (1, 2, 2, 64, 100, 136, 100, True, torch.float32, ""),       # fp32: 136 / 100 (wide fp32 kernel 256)
     (1, 4, 2, 128, 128, 100, 100, False, torch.bfloat16, "native_fp8"),  # 100 -> 104 -> 128 on the fp8 kernel
 ])
 def test_head_dims_off_the_kernel_grid_are_zero_padded(B, Hq, Hkv, Sq, Sk, D, Dv, causal, dtype, opt):

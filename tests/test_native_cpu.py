@@ -76,7 +76,7 @@ def _last_error():
     (dict(D=520, Dv=520), 2, "exceeds 512"),
     (dict(Dv=64, dtype=2, o_dtype=0, q_descale=0x10000, k_descale=0x10000, v_descale=0x10000), 2,
      "bf16/fp16/fp32 only"),                                         # D != Dv: not for fp8 codes
-    (dict(D=136, Dv=136, dtype=3, o_dtype=3), 2, "fp32 head dims"),  # fp32: up to 128
+    (dict(D=520, Dv=520, dtype=3, o_dtype=3), 2, "fp32 head dims"),  # fp32: up to 512
     (dict(D=96, Dv=66, dtype=3, o_dtype=3), 2, "multiples of 4"),    # fp32: multiples of 4
     (dict(D=96, Dv=96, dtype=2, o_dtype=0, q_descale=0x10000, k_descale=0x10000, v_descale=0x10000), 2,
      "head dim"),                                                    # fp8: 64 or 128
