@@ -6,7 +6,7 @@ S=2048, D=128, bf16), inputs resident in HBM.  ``value`` is algorithmic TFLOP/s 
 4*B*Hq*D*S(S+1)/2) over the timed steps.  Also reported, each on its own synthetic inputs: split-KV
 decode HBM GB/s (B=64, Hq=32, Hkv=8, D=128, lengths U[512, 8192]) with a contiguous and a paged cache,
 one decode step (KV-cache append of one token + decode), eager and as a HIP graph replay, the ring step (4 blocks + LSE merge), MMDiT
-joint attention in bf16 and fp8, the VAE attention (one head of 512), the small causal MHA case in fp32
+joint attention in bf16 and fp8, the VAE attention (one head of 512, in bf16 and in fp32), the small causal MHA case in fp32
 and bf16, and fp32 prefill on the headline shape.  The CPU baseline is
 libtorch's CPU SDPA (the call SdpaOp::Compute makes on a CPU mesh) on the same prefill, in fp32 on the
 bf16-rounded inputs (and in bf16 beside it), timed on this host over about ten seconds of repetitions,
@@ -354,6 +354,12 @@ def secondary_workloads(torch, F, dev, timer, cpu_info=None, cpu_seconds=0.0):
     extras["vae_attention_d512"] = {"TFLOP/s": round(fv / med / 1e12, 1), "frac_bf16": round(fv / med / PEAK_BF16, 4),
                                     "us": round(med * 1e6, 1)}
     log(f"VAE attention 1x1x16384 D=512: {fv / med / 1e12:.0f} TFLOP/s")
+    # the same attention run in fp32 (a port that keeps the VAE in fp32): the wide fp32 kernel
+    qv5, kv5, vv5 = (x.float() for x in (qv5, kv5, vv5))
+    med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(qv5, kv5, vv5), reps=3)
+    extras["vae_attention_d512_fp32"] = {"TFLOP/s": round(fv / med / 1e12, 1),
+                                         "frac_fp32": round(fv / med / PEAK_FP32, 4), "us": round(med * 1e6, 1)}
+    log(f"VAE attention 1x1x16384 D=512, fp32: {fv / med / 1e12:.1f} TFLOP/s ({fv / med / PEAK_FP32 * 100:.1f}% of fp32 peak)")
     del qv5, kv5, vv5
 
     # the CPU-runnable causal MHA case (B=1, H=8, S=512, D=64) in its own dtype, fp32, and in bf16
