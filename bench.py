@@ -404,7 +404,7 @@ def main():
                     help="first run 3 device copies of 1 GiB (known traffic) to scale rocprof byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the attention "
+        print(f"bench.py: measures one GPU only (asked for --gpus {args.gpus}); the attention "
               "operator is not sharded across GPUs here.", file=sys.stderr)
         sys.exit(2)
 

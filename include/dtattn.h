@@ -177,8 +177,9 @@ int dtattn_decode_splitkv_noalloc(const dtattn_decode_args* args, void* stream);
 
 /* Split-KV single-token decode against a paged KV cache.
  *
- * No counterpart in the reference (the next step its survey lists for decode: a KV cache feeding the
- * decode operator, python/dtorch/test/modules/llama.py:126-156).  Same arithmetic as
+ * No counterpart in the reference, whose Llama attention (python/dtorch/test/modules/llama.py:126-156)
+ * keeps no KV cache and attends over the whole sequence on every call: a paged KV cache feeding the
+ * decode operator.  Same arithmetic as
  * dtattn_decode_splitkv; token t of sequence b lives in page block_table[b][t / page_size] at row
  * t % page_size.  Page ids are clamped to [0, num_pages), so a corrupt block table reads wrong rows
  * but never leaves the pool.  Rows at or past lengths[b] never enter the result; with bf16/fp16 rows
