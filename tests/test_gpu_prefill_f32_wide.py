@@ -107,3 +107,29 @@ def test_prefill_f32_wide_ring_block_offsets_and_scale():
     o, lse, ro, rl = _run(q, k, v, causal=True, scale=0.07, q_offset=96, k_offset=48)
     assert max_abs(o, ro) <= O_TOL_F32
     assert lse_rel(lse, rl) <= LSE_TOL_F32
+
+
+def test_prefill_f32_wide_empty_and_single_key():
+    # no keys: O = 0 and LSE = -inf (the rows see nothing); one key: O = v, LSE = the one score
+    F = _F()
+    q = _dev(np.ones((1, 2, 40, 512), dtype=np.float32))
+    k0 = torch.zeros(1, 2, 0, 512, dtype=torch.float32, device="cuda")
+    o, lse = F.scaled_dot_product_attention_with_lse(q, k0, k0)
+    torch.cuda.synchronize()
+    assert o.shape == (1, 2, 40, 512) and bool((o == 0).all()) and bool(torch.isneginf(lse).all())
+    q, k, v = _qkv(70, 1, 2, 2, 40, 1, 256)
+    o, lse, ro, rl = _run(q, k, v)
+    assert max_abs(o, ro) <= O_TOL_F32 and lse_rel(lse, rl) <= LSE_TOL_F32
+
+
+def test_prefill_f32_wide_fully_masked_rows():
+    # rows whose mask hides every key get O = 0 and LSE = -inf, as in every other kernel
+    B, H, S, D = 1, 2, 70, 512
+    q, k, v = _qkv(80, B, H, H, S, S, D)
+    keep = np.ones((B, 1, S, S), dtype=bool)
+    keep[0, 0, 5] = False
+    keep[0, 0, 66] = False
+    o, lse, ro, rl = _run(q, k, v, mask_dev=torch.from_numpy(keep).cuda(), mask_ref=keep)
+    assert np.all(o[0, :, 5] == 0) and np.all(np.isneginf(lse[0, :, 5]))
+    ok = ~np.isneginf(rl)
+    assert max_abs(o, ro) <= O_TOL_F32 and lse_rel(lse[ok], rl[ok]) <= LSE_TOL_F32
