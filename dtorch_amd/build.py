@@ -24,7 +24,7 @@ BUILD = os.path.join(ROOT, "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["prefill_fwd.hip", "prefill_f32.hip", "prefill_wide.hip", "prefill_fp8.hip", "decode_splitkv.hip", "lse_merge.hip", "fp8_quant.hip", "kv_append.hip",
+HIP_SOURCES = ["prefill_fwd.hip", "prefill_rows64.hip", "prefill_f32.hip", "prefill_wide.hip", "prefill_fp8.hip", "decode_splitkv.hip", "lse_merge.hip", "fp8_quant.hip", "kv_append.hip",
                "dtattn_abi.cpp"]
 HOST_SOURCES = ["host/sdpa_op.cc", "host/bindings.cc"]
 
@@ -32,7 +32,7 @@ HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-mcode-object-version=5",
     # packed-fp32 VALU forms are disabled for every HIP translation unit
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wall", "-Wno-unused-function", f"-I{INCLUDE}", f"-I{CSRC}",
+    "-Wall", "-Wno-unused-function", f"-I{INCLUDE}", f"-I{CSRC}", f"-I{BUILD}",
 ]
 
 # Per-file flags.  The D = 512 wide-head kernel runs one wave per SIMD with 256 VGPRs and AGPRs beside them;
@@ -58,8 +58,15 @@ def _hipcc():
     return p
 
 
+def generate_sources() -> None:
+    """Sources written by generators: the tile-loop programs of prefill_rows64.hip."""
+    os.makedirs(BUILD, exist_ok=True)
+    _run([sys.executable, os.path.join(CSRC, "gen_prefill_rows64.py"), os.path.join(BUILD, "prefill_rows64_asm.inc")])
+
+
 def build_library(jobs: int = 8) -> str:
     os.makedirs(BUILD, exist_ok=True)
+    generate_sources()
     hipcc = _hipcc()
     objs = []
     cmds = []

