@@ -490,7 +490,7 @@ def main():
                    "Hkv": Hkv, "S": S, "D": D, "causal": True, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": profiled_traffic(),
-                     "kernel": "prefill_rows64_kernel<bf16,causal,2 waves>",
+                     "kernel": "prefill_rows64_gqa_kernel<bf16,causal>",
                      "work_per_launch": f"{flops} FLOP (4*B*Hq*D*S(S+1)/2)",
                      "avg_launch_us": round(k_avg * 1e6, 2)},
     }
