@@ -42,7 +42,7 @@ HEADLINE_SETTLE_S = 0.25  # minimum untimed back-to-back headline launches befor
 
 # HBM bytes per launch of the headline kernel, from the two calibrated rocprofv3 --pmc runs
 # (FETCH_SIZE, WRITE_SIZE) summarised in this file.
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "prefill_fwd_causal_gqa_b4_s2048_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "prefill_rows64_gqa_causal_b4_s2048_traffic.md")
 
 
 def log(*a):
