@@ -24,7 +24,7 @@ BUILD = os.path.join(ROOT, "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["prefill_fwd.hip", "prefill_rows64.hip", "prefill_f32.hip", "prefill_wide.hip", "prefill_fp8.hip", "decode_splitkv.hip", "lse_merge.hip", "fp8_quant.hip", "kv_append.hip",
+HIP_SOURCES = ["prefill_fwd.hip", "prefill_rows64.hip", "prefill_f32.hip", "prefill_wide.hip", "prefill_wide512.hip", "prefill_fp8.hip", "decode_splitkv.hip", "lse_merge.hip", "fp8_quant.hip", "kv_append.hip",
                "dtattn_abi.cpp"]
 HOST_SOURCES = ["host/sdpa_op.cc", "host/bindings.cc"]
 
@@ -59,9 +59,10 @@ def _hipcc():
 
 
 def generate_sources() -> None:
-    """Sources written by generators: the tile-loop programs of prefill_rows64.hip."""
+    """Sources written by generators: the tile-loop programs of prefill_rows64.hip and prefill_wide512.hip."""
     os.makedirs(BUILD, exist_ok=True)
     _run([sys.executable, os.path.join(CSRC, "gen_prefill_rows64.py"), os.path.join(BUILD, "prefill_rows64_asm.inc")])
+    _run([sys.executable, os.path.join(CSRC, "gen_prefill_wide512.py"), os.path.join(BUILD, "prefill_wide512_asm.inc")])
 
 
 def build_library(jobs: int = 8) -> str:

@@ -446,9 +446,15 @@ int wide_key_splits(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int D, int cu
     return n > 1 ? (int)n : 1;
 }
 
+bool prefill_wide512_fits(const PrefillParams& p);
+int prefill_wide512(const PrefillParams& p, bool f16, hipStream_t stream);
+
 // Entry from dtattn_prefill_fwd for kernel head dims 256 / 512 with bf16 or fp16 inputs.  p.nsplit and
-// p.kblock are set by the caller (1 and Sk when unsplit).
+// p.kblock are set by the caller (1 and Sk when unsplit).  Non-causal head-dim-512 calls without mask or
+// padding run the software-pipelined kernel of prefill_wide512.hip (the same arithmetic).
 int prefill_wide(const PrefillParams& p, int D, bool causal, bool bf16, bool pad, hipStream_t stream) {
+    if (D == 512 && !causal && !pad && p.mask == nullptr && prefill_wide512_fits(p))
+        return prefill_wide512(p, !bf16, stream);
     return bf16 ? dispatch_wide<bf16_t>(p, D, causal, pad, stream) : dispatch_wide<f16_t>(p, D, causal, pad, stream);
 }
 
