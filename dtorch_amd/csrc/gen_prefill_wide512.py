@@ -8,11 +8,12 @@ dependent phases (partial scores, exchange, softmax, PV) with no overlap, at one
 step of the loop runs, for tile t:
 
   phase A:  S(t+1) partial = K(t+1) Q^T (16 MFMAs, K fragments read four ahead)
-            || the partner's partial of S(t), the row max, the lazy-rescale decision and P(t) (VALU), and
-               the loads of K(t+2) and V(t+1) (one per MFMA)
+            || the partner's partial of S(t), the row max, the lazy-rescale decision and the first half of
+               P(t) (VALU), and the loads of K(t+2) (one per MFMA)
   (rare)    O *= alpha
-  phase B:  O^T += V(t)^T P(t)^T (16 MFMAs, V^T fragments read four ahead), then this wave's partial of
-            S(t+1) into the exchange slab of the other parity
+  phase B:  O^T += V(t)^T P(t)^T (16 MFMAs, V^T fragments read four ahead)
+            || the second half of P(t), due before the MFMAs that read it, and the loads of V(t+1); then this
+               wave's partial of S(t+1) into the exchange slab of the other parity
   one barrier per step.
 
 The arithmetic is that of prefill_wide_kernel element for element (the same MFMA accumulation order, the
@@ -203,16 +204,22 @@ class Program:
         ex = [f"v_exp_f32 v{x}, v{x}" for x in r]
         add = [f"v_add_f32 %[l], %[l], v{x}" for x in r]
         cvt = [f"{self.cvt} v{P(j // 4) + j % 4}, v{r[2 * j]}, v{r[2 * j + 1]}" for j in range(8)]
-        for st in range(18):
-            if st < 16:
-                out.append(fma[st])
-            if 1 <= st <= 16:
-                out.append(ex[st - 1])
-            if st >= 2:
-                out.append(add[st - 2])
-                if (st - 2) % 2 == 1:
-                    out.append(cvt[(st - 2) // 2])
-        return out
+        def chain(lo, hi):
+            res = []
+            for st in range(lo, hi + 2):
+                if st < hi:
+                    res.append(fma[st])
+                if lo + 1 <= st <= hi:
+                    res.append(ex[st - 1])
+                if st >= lo + 2:
+                    res.append(add[st - 2])
+                    if (st - 2) % 2 == 1:
+                        res.append(cvt[(st - 2) // 2])
+            return res
+        if last:
+            return out + chain(0, 16), []
+        # the second half of P (PV k-step 1) is finished in phase B, before the MFMAs that read it
+        return out + chain(0, 8), chain(8, 16)
 
     def mask_code(self, b):
         """Keys at or past Sk -> -inf (only a block's last tile can hold them): element i of a lane is key
@@ -279,8 +286,11 @@ class Program:
                 self.e(*dma[f])
             self.e(*sl[f])
 
-    def phase_b(self, vb, slab):
-        """O^T += V(buffer vb)^T P^T; then (slab = (parity, S buffer)) this wave's partial into the slab."""
+    def phase_b(self, vb, slab, dma=None, valu=()):
+        """O^T += V(buffer vb)^T P^T, with one load pair per MFMA (dma) and VALU (the second half of P) in the
+        first six slots, two MFMAs ahead of the k-step that reads it; then (slab = (parity, S buffer)) this
+        wave's partial into the slab."""
+        sl = self.slots(list(valu), 6) + [[] for _ in range(10)] if valu else [[] for _ in range(16)]
         for m in range(16):
             ks, dt = m >> 3, m & 7
             self.e(self.lds.wait_for(("V", vb, m)))
@@ -288,6 +298,9 @@ class Program:
             self.e(f"{self.mfma} {o}, {vr(VT(m % self.va), 4)}, {vr(P(ks), 4)}, {o}")
             if m + self.va < 16:
                 self.e(*self.vread(vb, m + self.va))
+            if dma and m < len(dma):
+                self.e(*dma[m])
+            self.e(*sl[m])
             if m == 12 and slab is not None:
                 self.e(*self.slab_write(*slab))
 
@@ -303,18 +316,18 @@ class Program:
         lb = f"L{u}_%="
         self.e("s_add_i32 s46, s40, 1", "s_cmp_lt_i32 s46, %[nt]", f"s_cbranch_scc0 {lb}_last")
         self.e(*self.dma_setup("V", "s46"), "s_add_i32 s46, s40, 2", *self.dma_setup("K", "s46"))
-        dma = self.dma_loads("K", par) + self.dma_loads("V", 1 - par)
         self.e(*self.partner_read(par))
-        self.phase_a(1 - par, 1 - par, self.softmax_valu(par, False), dma, par)
+        va, vb = self.softmax_valu(par, False)
+        self.phase_a(1 - par, 1 - par, va, self.dma_loads("K", par), par)
         self.rescale(f"{lb}_r")
-        self.phase_b(par, (1 - par, 1 - par))
+        self.phase_b(par, (1 - par, 1 - par), self.dma_loads("V", 1 - par), vb)
         self.step_end()
         self.e(f"s_branch {lb}_next", f"{lb}_last:")
         # a block's last tile: no next scores, no loads
         self.lds.drain()
         self.e(*self.partner_read(par))
         self.e(self.lds.wait_for(("PT", 3)))
-        self.e(*self.softmax_valu(par, True))
+        self.e(*self.softmax_valu(par, True)[0])
         self.rescale(f"{lb}_q")
         self.e(*[x for m in range(self.va) for x in self.vread(par, m)])
         self.phase_b(par, None)
