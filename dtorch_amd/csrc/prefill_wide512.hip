@@ -211,11 +211,13 @@ __global__ void __launch_bounds__(256, 1) prefill_wide512_kernel(const PrefillPa
     }
 }
 
-// Whether a call can take the pipelined kernel: a positive scale (Q is loaded untransformed) and 32-bit
-// byte offsets for a tile's rows.
+// Whether a call can take the pipelined kernel: a positive scale (Q is loaded untransformed), and every tile's
+// byte offset from the head's first key row in 32 bits: the program computes it as one 32-bit scalar product
+// (32 j) * pitch for tiles j up to two past the last.
 bool prefill_wide512_fits(const PrefillParams& p) {
     const int64_t pitch = (p.ks_s > p.vs_s ? p.ks_s : p.vs_s) * 2;
-    return p.q_and == 0xffffffffu && p.q_xor == 0u && p.ks_s >= 0 && p.vs_s >= 0 && 32 * pitch < ((int64_t)1 << 31);
+    return p.q_and == 0xffffffffu && p.q_xor == 0u && p.ks_s >= 0 && p.vs_s >= 0 &&
+           ((int64_t)p.Sk + 64) * pitch < ((int64_t)1 << 31);
 }
 
 template <typename T>

@@ -85,6 +85,32 @@ def test_wide512_strided_layout_and_negative_scale():
     assert lse_rel(host(lse), rl) <= LSE_TOL
 
 
+def test_wide512_key_offsets_past_31_bits_take_the_unpipelined_kernel():
+    # K and V rows 2 MiB apart (two views of one 2.1 GB buffer): (Sk + 64) * pitch >= 2^31, so a tile's byte
+    # offset no longer fits the program's 32-bit scalar arithmetic and the call must take prefill_wide_kernel,
+    # whose outputs equal the pipelined kernel's on contiguous copies of the same K and V bit for bit
+    rng = np.random.default_rng(23)
+    Sq, Sk, pitch = 128, 1000, 1 << 20
+    assert (Sk + 64) * pitch * 2 >= 1 << 31
+    q, k, v = randn(rng, (1, 1, Sq, 512)), randn(rng, (1, 1, Sk, 512)), randn(rng, (1, 1, Sk, 512))
+    tq, tk, tv = to_dev(q), to_dev(k), to_dev(v)
+    buf = torch.zeros(Sk * pitch, dtype=torch.bfloat16, device=tq.device)
+    sk = torch.as_strided(buf, (1, 1, Sk, 512), (0, 0, pitch, 1), 0)
+    sv = torch.as_strided(buf, (1, 1, Sk, 512), (0, 0, pitch, 1), 512)
+    sk.copy_(tk)
+    sv.copy_(tv)
+    F = _F()
+    o, lse = F.scaled_dot_product_attention_with_lse(tq, sk, sv)
+    o2, lse2 = F.scaled_dot_product_attention_with_lse(tq, tk, tv)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2)
+    assert torch.equal(lse, lse2)
+    ro, rl = orc.sdpa_fwd(rounded(q), rounded(k), rounded(v))
+    assert max_abs(host(o), ro) <= O_TOL_BF16
+    assert lse_rel(host(lse), rl) <= LSE_TOL
+    del buf, sk, sv
+
+
 def test_wide512_vae_16k_sampled_rows():
     # the VAE shape itself (128 x 128 latent pixels): the first and last row of every 64-row workgroup
     rng = np.random.default_rng(22)
