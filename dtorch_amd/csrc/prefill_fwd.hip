@@ -388,16 +388,18 @@ static int dispatch_prefill_m(const PrefillParams& p, int D, bool causal, hipStr
     return fail(DTATTN_ERR_UNSUPPORTED, "prefill: kernel head dim %d not supported (64, 128, 256 or 512)", D);
 }
 
-int prefill_rows64(const PrefillParams& p, bool causal, bool f16, hipStream_t stream);
+int prefill_rows64(const PrefillParams& p, bool causal, bool f16, void* ws, size_t ws_bytes, hipStream_t stream);
 bool prefill_rows64_fits(const PrefillParams& p);
+size_t rows64_sk_workspace(const dtattn_prefill_args* a, int device);
 
 // D is the kernel's head dim (64 or 128); pad: the real head dims are below it.  Head dim 128 without mask or
 // padding runs the 64-rows-per-wave kernel (prefill_rows64.hip), which returns the same bits as
 // prefill_fwd_kernel at 4-9% (non-causal) and 4-14% (causal) more throughput.
 template <typename T>
-static int dispatch_prefill(const PrefillParams& p, int D, bool causal, bool pad, hipStream_t stream) {
+static int dispatch_prefill(const PrefillParams& p, int D, bool causal, bool pad, void* ws, size_t ws_bytes,
+                            hipStream_t stream) {
     if (D == 128 && !pad && p.mask == nullptr && prefill_rows64_fits(p))
-        return prefill_rows64(p, causal, __is_same(T, f16_t), stream);
+        return prefill_rows64(p, causal, __is_same(T, f16_t), ws, ws_bytes, stream);
     if (pad)
         return p.mask != nullptr ? dispatch_prefill_m<T, true, true>(p, D, causal, stream)
                                  : dispatch_prefill_m<T, false, true>(p, D, causal, stream);
@@ -623,8 +625,8 @@ extern "C" int dtattn_prefill_fwd(const dtattn_prefill_args* a, void* stream_) {
         m.o_dtype = a->o_dtype;
         return dtattn_lse_merge(&m, stream);
     }
-    if (a->dtype == DTATTN_BF16) return dispatch_prefill<bf16_t>(p, Dk, causal, pad, stream);
-    return dispatch_prefill<f16_t>(p, Dk, causal, pad, stream);
+    if (a->dtype == DTATTN_BF16) return dispatch_prefill<bf16_t>(p, Dk, causal, pad, a->workspace, a->workspace_bytes, stream);
+    return dispatch_prefill<f16_t>(p, Dk, causal, pad, a->workspace, a->workspace_bytes, stream);
 }
 
 extern "C" size_t dtattn_prefill_workspace_size(const dtattn_prefill_args* a) {
@@ -634,5 +636,6 @@ extern "C" size_t dtattn_prefill_workspace_size(const dtattn_prefill_args* a) {
     if (a->dtype == DTATTN_FP8_E4M3FN) return prefill_fp8_workspace_size(a, dev);
     size_t bytes = 0, lse_off = 0;
     wide_plan(a, dev, &bytes, &lse_off);
-    return bytes;
+    const size_t sk = rows64_sk_workspace(a, dev);
+    return bytes > sk ? bytes : sk;
 }

@@ -21,6 +21,8 @@
 // prefill_rows64_kernel: NW waves x 64 consecutive rows of one (batch, query head), NW = 2 for causal calls
 // (two workgroups per CU), 4 otherwise.  K and V tiles of 64 keys are double-buffered in LDS and filled by
 // direct buffer->LDS loads spread over phase A; the epilogue is prefill_fwd_kernel's.
+#include <cmath>
+
 #include "dtattn_common.hpp"
 #include "prefill_params.hpp"
 #include "prefill_rows64_asm.inc"
@@ -448,6 +450,326 @@ __global__ void __launch_bounds__(256, 1) prefill_rows64_gqa_kernel(const Prefil
     }
 }
 
+// Stream-K form of the row layout (non-causal, positive scale).  A grid of n_items workgroups of 256 rows
+// (4 waves x 64 consecutive rows of one head) that does not fill whole rounds of the CUs leaves part of the
+// chip idle in its last round: C5a's 432 items on 256 CUs run as 1.69 rounds in the time of 2.  Here one
+// workgroup per CU takes an equal, contiguous share of all (item, key tile) units, items in order with the
+// query block fastest, and runs it as segments: whole items end in the usual epilogue, and the at most two
+// segments of a share that cut an item (its first and its last) leave their unnormalised O, row max and
+// row sums in a workspace record, which a second launch merges by the row maxima.  Shares are dealt XCD by
+// XCD (workgroup w on XCD w % 8 takes share (w % 8) G/8 + w / 8), so an XCD walks consecutive row blocks of
+// the same heads and their K/V stay in its L2.
+struct Rows64Sk {
+    int64_t units;  // n_items * nt
+    int32_t nt;     // key tiles per item
+    int32_t nqb;    // 256-row query blocks per head
+    int32_t G;      // workgroups (a multiple of 8)
+    float* ws;      // 2 G records of kRows64SkRec floats
+};
+// One record: lane l of wave w holds O / l of its 128 accumulators (the epilogue's order: float4 16 X + 4 dt + i4
+// at (32 w + 16 X + 4 dt + i4) 64 + l), then its rows' (max A, max B, sum A, sum B) at float4 4 * 64 * 32 + 64 w
+// + l.
+constexpr int kRows64SkRec = 4 * 64 * 128 + 4 * 64 * 4;
+
+__device__ __forceinline__ int64_t sk_start(int64_t units, int G, int r) { return units * r / G; }
+
+template <typename T>
+__global__ void __launch_bounds__(256, 1) prefill_rows64_sk_kernel(const PrefillParams p, const Rows64Sk sk) {
+    typedef typename Elem<T>::vec4 V4;
+    constexpr int D = 128, BN = 64, DCH = 16, INSTR = 4;
+    __shared__ __attribute__((aligned(16))) T smem[4 * BN * D];    // K0, K1, V0, V1
+    __shared__ __attribute__((aligned(16))) T ostage[4 * 64 * D];  // O staging: 64 rows per wave
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31;
+    const int hf = lane >> 5;
+    const int G = sk.G;
+    const int rank = (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3);
+    const int64_t u0 = sk_start(sk.units, G, rank), u1 = sk_start(sk.units, G, rank + 1);
+    if (u0 >= u1) return;  // workgroup-uniform
+
+    const int krow = (int)(p.ks_s * (int64_t)sizeof(T));
+    const int vrow = (int)(p.vs_s * (int64_t)sizeof(T));
+    const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+    u32x8 doff;
+#pragma unroll
+    for (int i = 0; i < INSTR; ++i) {
+        const int r = (wave * INSTR + i) * 4 + lane / DCH;
+        const int cc = (lane % DCH) ^ kswz128(r);
+        doff[i] = (uint32_t)(r * krow + cc * 16);
+        doff[INSTR + i] = (uint32_t)(r * vrow + cc * 16);
+    }
+    const uint32_t m0base = __builtin_amdgcn_readfirstlane(sbase + (uint32_t)(wave * INSTR * 1024));
+
+    // segment: tiles t0 .. t1-1 of item i (this wave: rows q0 .. q0+63 of head hq); its keys start at key
+    // 64 t0, so K/V are addressed from there and the program sees skr = Sk - 64 t0 keys
+    struct Seg {
+        int b, hq, q0, nt, skr, slot;
+        bool whole;
+        const T *qp, *kp, *vp;
+    };
+    auto seg_at = [&](int64_t u) {
+        Seg s;
+        const int i = (int)(u / sk.nt);
+        const int t0 = (int)(u - (int64_t)i * sk.nt);
+        const int t1 = (int)min((int64_t)sk.nt, (int64_t)t0 + (u1 - u));
+        const int qb = i % sk.nqb, bh = i / sk.nqb;
+        s.b = bh / p.Hq;
+        s.hq = bh % p.Hq;
+        const int hk = s.hq / p.group;
+        s.q0 = qb * 256 + wave * 64;
+        s.nt = t1 - t0;
+        s.skr = p.Sk - t0 * BN;
+        s.whole = t0 == 0 && t1 == sk.nt;
+        s.slot = 2 * rank + (u == u0 ? 0 : 1);
+        s.qp = reinterpret_cast<const T*>(p.q) + s.b * p.qs_b + s.hq * p.qs_h;
+        s.kp = reinterpret_cast<const T*>(p.k) + s.b * p.ks_b + hk * p.ks_h + (int64_t)t0 * BN * p.ks_s;
+        s.vp = reinterpret_cast<const T*>(p.v) + s.b * p.vs_b + hk * p.vs_h + (int64_t)t0 * BN * p.vs_s;
+        return s;
+    };
+    auto dma = [&](int buf, const T* base, int pitch, int64_t stride, int t, int skr, int first) {
+        const int rows = min(BN, skr - t * BN);
+        const uint32_t nbytes = (uint32_t)((rows - 1) * pitch + D * (int)sizeof(T));
+        const auto rs = make_rsrc(base + (int64_t)t * BN * stride, nbytes);
+        T* dst = smem + buf * BN * D;
+#pragma unroll
+        for (int i = 0; i < INSTR; ++i) buf_ld16_lds_async(rs, dst + (wave * INSTR + i) * 4 * D, doff[first + i]);
+    };
+    u32x32 QA, QB;
+    auto prefetch = [&](const Seg& s) {
+        dma(0, s.kp, krow, p.ks_s, 0, s.skr, 0);
+        dma(2, s.vp, vrow, p.vs_s, 0, s.skr, INSTR);
+        if (s.nt > 1) dma(1, s.kp, krow, p.ks_s, 1, s.skr, 0);
+        const T* qa = s.qp + (int64_t)min(s.q0 + l32, p.Sq - 1) * p.qs_s + hf * 8;
+        const T* qb = s.qp + (int64_t)min(s.q0 + 32 + l32, p.Sq - 1) * p.qs_s + hf * 8;
+        asm volatile(
+            "global_load_dwordx4 a[128:131], %2, off\n\tglobal_load_dwordx4 a[132:135], %2, off offset:32\n\t"
+            "global_load_dwordx4 a[136:139], %2, off offset:64\n\tglobal_load_dwordx4 a[140:143], %2, off offset:96\n\t"
+            "global_load_dwordx4 a[144:147], %2, off offset:128\n\tglobal_load_dwordx4 a[148:151], %2, off offset:160\n\t"
+            "global_load_dwordx4 a[152:155], %2, off offset:192\n\tglobal_load_dwordx4 a[156:159], %2, off offset:224\n\t"
+            "global_load_dwordx4 a[160:163], %3, off\n\tglobal_load_dwordx4 a[164:167], %3, off offset:32\n\t"
+            "global_load_dwordx4 a[168:171], %3, off offset:64\n\tglobal_load_dwordx4 a[172:175], %3, off offset:96\n\t"
+            "global_load_dwordx4 a[176:179], %3, off offset:128\n\tglobal_load_dwordx4 a[180:183], %3, off offset:160\n\t"
+            "global_load_dwordx4 a[184:187], %3, off offset:192\n\tglobal_load_dwordx4 a[188:191], %3, off offset:224"
+            : "={a[128:159]}"(QA), "={a[160:191]}"(QB)
+            : "v"(qa), "v"(qb)
+            : "memory");
+    };
+
+    int64_t u = u0;
+    Seg s = seg_at(u);
+    prefetch(s);
+    while (true) {
+        u32x16 addr;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) addr[ks] = sbase + (uint32_t)(l32 * D + 8 * ((2 * ks + hf) ^ kswz128(l32))) * 2u;
+        {
+            const int blk = lane >> 4, bl = lane & 15;
+            const int tr_key = bl >> 2, tr_d = 16 * (blk & 1) + 4 * (bl & 3), tr_k4 = 4 * (blk >> 1);
+            const int k1 = tr_k4 + tr_key, k2 = k1 + 8;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const int d = dt * 32 + tr_d;
+                addr[8 + dt] = sbase + (uint32_t)(k1 * D + 8 * ((d >> 3) ^ kswz128(k1)) + (d & 7)) * 2u;
+                addr[12 + dt] = sbase + (uint32_t)(k2 * D + 8 * ((d >> 3) ^ kswz128(k2)) + (d & 7)) * 2u;
+            }
+        }
+        u32x2 lim;
+        lim[0] = lim[1] = (uint32_t)(s.skr - 1 - 4 * hf);
+        f32x32 OA01, OA23, OB01, OB23;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) OA01[i] = 0.f, OA23[i] = 0.f, OB01[i] = 0.f, OB23[i] = 0.f;
+        float mA = kNegInf, mB = kNegInf, lA = 0.f, lB = 0.f;
+        const float c = p.c;
+        const int kd = 0;  // causal offsets only
+        const int nt = __builtin_amdgcn_readfirstlane(s.nt), tw = nt;
+        const int skr = __builtin_amdgcn_readfirstlane(s.skr);
+        const uint64_t kb64 = (uint64_t)(uintptr_t)s.kp, vb64 = (uint64_t)(uintptr_t)s.vp;
+        const uint32_t klo = __builtin_amdgcn_readfirstlane((uint32_t)kb64);
+        const uint32_t khi = __builtin_amdgcn_readfirstlane((uint32_t)(kb64 >> 32));
+        const uint32_t vlo = __builtin_amdgcn_readfirstlane((uint32_t)vb64);
+        const uint32_t vhi = __builtin_amdgcn_readfirstlane((uint32_t)(vb64 >> 32));
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this segment's Q and first tiles (and the last stores)
+        lds_barrier();
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is named as clobbered: the program sets it for its loads
+#define DTATTN_ROWS64_SK_OPERANDS                                                                              \
+    : "+{a[0:31]}"(OA01), "+{a[32:63]}"(OA23), "+{a[64:95]}"(OB01), "+{a[96:127]}"(OB23), [mA] "+v"(mA),       \
+      [mB] "+v"(mB), [lA] "+v"(lA), [lB] "+v"(lB)                                                                \
+    : "{a[128:159]}"(QA), "{a[160:191]}"(QB), "{v[200:215]}"(addr), [nt] "s"(nt), [tw] "s"(tw), [c] "s"(c),    \
+      [sk] "s"(skr), [kd] "s"(kd), [kp] "s"(krow), [vp] "s"(vrow), [klo] "s"(klo), [khi] "s"(khi),             \
+      [vlo] "s"(vlo), [vhi] "s"(vhi), [m0base] "s"(m0base), "{v[216:223]}"(doff), "{v[224:225]}"(lim)
+        if constexpr (__is_same(T, f16_t)) asm volatile(DTATTN_ROWS64_PROGRAM_F16_4_0 DTATTN_ROWS64_SK_OPERANDS : DTATTN_ROWS64_CLOBBERS);
+        else asm volatile(DTATTN_ROWS64_PROGRAM_BF16_4_0 DTATTN_ROWS64_SK_OPERANDS : DTATTN_ROWS64_CLOBBERS);
+#undef DTATTN_ROWS64_SK_OPERANDS
+#pragma clang diagnostic pop
+        // every wave is past its last K/V read: the buffers take the next segment's tiles during this epilogue
+        lds_barrier();
+        const Seg cur = s;
+        u += cur.nt;
+        const bool more = u < u1;
+        if (more) {
+            s = seg_at(u);
+            prefetch(s);
+        }
+        if (!cur.whole) {
+            // a cut item: O over this segment's row sums, the row maxima and the row sums go to its record
+            f32x4* rec = reinterpret_cast<f32x4*>(sk.ws + (int64_t)cur.slot * kRows64SkRec);
+            float ls[2];
+#pragma unroll
+            for (int X = 0; X < 2; ++X) {
+                const float l = sum_xor32(X == 0 ? lA : lB);
+                const float inv = l > 0.f ? 1.f / l : 0.f;
+                ls[X] = l;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4) {
+                        f32x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int kk = 16 * (dt & 1) + 4 * i4 + e;
+                            const float ov = X == 0 ? (dt < 2 ? OA01[kk] : OA23[kk]) : (dt < 2 ? OB01[kk] : OB23[kk]);
+                            v[e] = ov * inv;
+                        }
+                        rec[(32 * wave + 16 * X + 4 * dt + i4) * 64 + lane] = v;
+                    }
+            }
+            rec[4 * 64 * 32 + 64 * wave + lane] = f32x4{mA, mB, ls[0], ls[1]};
+            if (!more) break;
+            continue;
+        }
+        // Epilogue of a whole item: prefill_rows64_gqa_kernel's, for this wave's rows of head cur.hq
+        T* Os = ostage + wave * 64 * D;
+#pragma unroll
+        for (int X = 0; X < 2; ++X) {
+            const float l = sum_xor32(X == 0 ? lA : lB);
+            const float m = X == 0 ? mA : mB;
+            const float inv = l > 0.f ? 1.f / l : 0.f;
+            const int row = 32 * X + l32;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    V4 o4;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int kk = 16 * (dt & 1) + 4 * i4 + e;
+                        const float ov = X == 0 ? (dt < 2 ? OA01[kk] : OA23[kk]) : (dt < 2 ? OB01[kk] : OB23[kk]);
+                        o4[e] = Elem<T>::from_f32(ov * inv);
+                    }
+                    const int cc = dt * 4 + i4;
+                    *reinterpret_cast<V4*>(Os + row * D + 8 * (cc ^ (row % DCH)) + 4 * hf) = o4;
+                }
+            if (p.lse != nullptr && hf == 0) {
+                const int qrow = cur.q0 + row;
+                if (qrow < p.Sq)
+                    p.lse[cur.b * p.lses_b + cur.hq * p.lses_h + qrow] = l > 0.f ? (m + __log2f(l)) * kLn2 : kNegInf;
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave reads back only its own staged rows
+        T* op = reinterpret_cast<T*>(p.o) + cur.b * p.os_b + cur.hq * p.os_h;
+#pragma unroll
+        for (int i = 0; i < 64 * DCH / 64; ++i) {
+            const int id = i * 64 + lane;
+            const int row = id / DCH, cc = id % DCH;
+            const int qrow = cur.q0 + row;
+            if (qrow < p.Sq)
+                __builtin_nontemporal_store(ld16(Os + row * D + 8 * (cc ^ (row % DCH))),
+                                            reinterpret_cast<u32x4*>(op + (int64_t)qrow * p.os_s + cc * 8));
+        }
+        if (!more) break;
+    }
+}
+
+// Merge of the items the shares cut.  Workgroup r - 1 takes the share boundary r; it merges the item that
+// boundary falls in (unless an earlier boundary falls in the same item), combining the records of every
+// share that covers part of it by their row maxima, in share order, then writes O and the LSE as the
+// epilogue of an uncut item would.
+template <typename T>
+__global__ void __launch_bounds__(256) rows64_sk_merge_kernel(const PrefillParams p, const Rows64Sk sk) {
+    typedef typename Elem<T>::vec4 V4;
+    constexpr int D = 128, DCH = 16;
+    __shared__ __attribute__((aligned(16))) T ostage[4 * 64 * D];
+    const int G = sk.G;
+    const int r = (int)blockIdx.x + 1;
+    const int64_t ub = sk_start(sk.units, G, r);
+    const int i = (int)(ub / sk.nt);
+    const int64_t ib = (int64_t)i * sk.nt, ie = ib + sk.nt;
+    if (ub == ib) return;                                   // the boundary is an item edge
+    if (r >= 2 && sk_start(sk.units, G, r - 1) > ib) return;  // an earlier boundary merges this item
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int hf = lane >> 5;
+    // running (M, L, o) per row block: o = sum_p l_p 2^(m_p - M) O_p, L = sum_p l_p 2^(m_p - M)
+    float o[128];
+    float mA = kNegInf, mB = kNegInf, lA = 0.f, lB = 0.f;
+#pragma unroll
+    for (int k = 0; k < 128; ++k) o[k] = 0.f;
+    for (int q = r - 1; q < G && sk_start(sk.units, G, q) < ie; ++q) {
+        const int slot = 2 * q + ((q == r - 1 && sk_start(sk.units, G, q) < ib) ? 1 : 0);
+        const f32x4* rec = reinterpret_cast<const f32x4*>(sk.ws + (int64_t)slot * kRows64SkRec);
+        const f32x4 ml = rec[4 * 64 * 32 + 64 * wave + lane];
+        const float nA = fmaxf(mA, ml[0]), nB = fmaxf(mB, ml[1]);
+        // a max of -inf carries no keys: weight 0
+        const float aA = mA == kNegInf ? 0.f : exp2f(mA - nA), bA = ml[0] == kNegInf ? 0.f : ml[2] * exp2f(ml[0] - nA);
+        const float aB = mB == kNegInf ? 0.f : exp2f(mB - nB), bB = ml[1] == kNegInf ? 0.f : ml[3] * exp2f(ml[1] - nB);
+        lA = lA * aA + bA;
+        lB = lB * aB + bB;
+        mA = nA;
+        mB = nB;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const f32x4 v = rec[(32 * wave + j) * 64 + lane];
+            const float a = j < 16 ? aA : aB, w = j < 16 ? bA : bB;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[4 * j + e] = o[4 * j + e] * a + v[e] * w;
+        }
+    }
+    // the item's rows and head, as the main kernel derives them
+    const int qb = i % sk.nqb, bh = i / sk.nqb;
+    const int b = bh / p.Hq, hq = bh % p.Hq;
+    const int q0 = qb * 256 + wave * 64;
+    T* Os = ostage + wave * 64 * D;
+#pragma unroll
+    for (int X = 0; X < 2; ++X) {
+        const float l = X == 0 ? lA : lB;  // whole row sums already
+        const float m = X == 0 ? mA : mB;
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        const int row = 32 * X + l32;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                V4 o4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o4[e] = Elem<T>::from_f32(o[64 * X + 16 * dt + 4 * i4 + e] * inv);
+                const int cc = dt * 4 + i4;
+                *reinterpret_cast<V4*>(Os + row * D + 8 * (cc ^ (row % DCH)) + 4 * hf) = o4;
+            }
+        if (p.lse != nullptr && hf == 0) {
+            const int qrow = q0 + row;
+            if (qrow < p.Sq) p.lse[b * p.lses_b + hq * p.lses_h + qrow] = l > 0.f ? (m + __log2f(l)) * kLn2 : kNegInf;
+        }
+    }
+    __syncthreads();
+    T* op = reinterpret_cast<T*>(p.o) + b * p.os_b + hq * p.os_h;
+#pragma unroll
+    for (int it = 0; it < 64 * DCH / 64; ++it) {
+        const int id = it * 64 + lane;
+        const int row = id / DCH, cc = id % DCH;
+        const int qrow = q0 + row;
+        if (qrow < p.Sq)
+            __builtin_nontemporal_store(ld16(Os + row * D + 8 * (cc ^ (row % DCH))),
+                                        reinterpret_cast<u32x4*>(op + (int64_t)qrow * p.os_s + cc * 8));
+    }
+}
+
 template <typename T, bool CAUSAL, int NW>
 static int launch_rows64(const PrefillParams& prm, hipStream_t stream) {
     PrefillParams p = prm;
@@ -485,9 +807,78 @@ static int launch_rows64_gqa(const PrefillParams& prm, int cus, hipStream_t stre
     return check_launch("prefill_rows64_gqa_kernel");
 }
 
-int prefill_rows64(const PrefillParams& p, bool causal, bool f16, hipStream_t stream) {
+// Shares of the stream-K form for a non-causal row-layout call (B, Hq, Sq, Sk) on `cus` CUs, and the workspace
+// its records need; false unless the model below says the shares beat the plain grid by 5%.  Times in key
+// tiles (of 256 rows x 64 keys on every CU): an item costs nt + 4 (Q load, first tiles, epilogue); a share
+// its tiles plus 4 per segment, plus 20 for writing and merging the records (~68 MB of fp32 at 256 CUs;
+// measured 16-27 on the shapes of the tests).  By it, 1 x 8 x 4096 (128 items on 256 CUs) gains 21% and
+// 1 x 24 x 4096 (384 items) 9%, while 1 x 24 x 4608 (432 items, 72 tiles each) keeps the plain grid: its
+// ragged round costs less than the records (stream-K measured 4-7% slower there).
+bool rows64_sk_plan(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int cus, Rows64Sk* sk, size_t* bytes) {
+    const int G = cus & ~7;
+    if (G < 8 || B <= 0 || Hq <= 0 || Sq <= 0 || Sk <= 0) return false;
+    const int64_t nqb = (Sq + 255) / 256, n_items = nqb * B * Hq, nt = (Sk + 63) / 64;
+    if (n_items > 0x7fffffff || n_items * nt > ((int64_t)1 << 40)) return false;
+    const int64_t units = n_items * nt;
+    const double per = (double)units / G;
+    if (per < 8.0) return false;
+    const double plain = (double)((n_items + G - 1) / G) * (double)(nt + 4);
+    const double segs = std::ceil(per / (double)nt) + 1.0;
+    if (std::ceil(per) + 4.0 * segs + 20.0 >= 0.95 * plain) return false;
+    sk->units = units;
+    sk->nt = (int32_t)nt;
+    sk->nqb = (int32_t)nqb;
+    sk->G = G;
+    sk->ws = nullptr;
+    *bytes = (size_t)2 * G * kRows64SkRec * sizeof(float);
+    return true;
+}
+
+// Workspace the stream-K form can use for a prefill call on `device` (0: the call does not take it): bf16 /
+// fp16 at head dims D = Dv = 128, non-causal, no mask, a positive scale, groups that are not multiples of 4
+// (those take the grouped-query form), and tile offsets that fit the program's 32-bit arithmetic.
+size_t rows64_sk_workspace(const dtattn_prefill_args* a, int device) {
+    if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16) return 0;
+    if (a->D != 128 || a->Dv != 128 || a->causal != 0 || a->mask != nullptr || a->scale <= 0.f) return 0;
+    if (a->Hkv <= 0 || a->Hq % a->Hkv != 0) return 0;
+    const int64_t group = a->Hq / a->Hkv;
+    if (group >= 4 && group % 4 == 0) return 0;
+    const int64_t ks = a->k_stride[2], vs = a->v_stride[2];
+    if (ks < 0 || vs < 0 || (a->Sk + 128) * (ks > vs ? ks : vs) * 2 >= ((int64_t)1 << 31)) return 0;
+    dtattn_device_peaks pk;
+    if (dtattn_get_device_peaks(device, &pk) != DTATTN_OK) return 0;
+    Rows64Sk sk;
+    size_t bytes = 0;
+    return rows64_sk_plan(a->B, a->Hq, a->Sq, a->Sk, pk.cu_count, &sk, &bytes) ? bytes : 0;
+}
+
+template <typename T>
+static int launch_rows64_sk(const PrefillParams& p, const Rows64Sk& sk, hipStream_t stream) {
+    hipLaunchKernelGGL((prefill_rows64_sk_kernel<T>), dim3((unsigned)sk.G), dim3(256), 0, stream, p, sk);
+    const int st = check_launch("prefill_rows64_sk_kernel");
+    if (st != DTATTN_OK) return st;
+    hipLaunchKernelGGL((rows64_sk_merge_kernel<T>), dim3((unsigned)(sk.G - 1)), dim3(256), 0, stream, p, sk);
+    return check_launch("rows64_sk_merge_kernel");
+}
+
+// ws / ws_bytes: the caller's workspace (may be NULL); non-causal row-layout calls whose grid would leave a
+// ragged last round take the stream-K form when it holds the records.
+int prefill_rows64(const PrefillParams& p, bool causal, bool f16, void* ws, size_t ws_bytes, hipStream_t stream) {
+    const bool positive = p.q_and == 0xffffffffu && p.q_xor == 0u;
+    const bool gqa_form = p.group >= 4 && p.group % 4 == 0;
+    if (!causal && !gqa_form && positive && ws != nullptr && (reinterpret_cast<uintptr_t>(ws) & 255u) == 0) {
+        int dev = 0;
+        dtattn_device_peaks pk;
+        Rows64Sk sk;
+        size_t need = 0;
+        if (rows64_stream_device(stream, &dev) == DTATTN_OK && dtattn_get_device_peaks(dev, &pk) == DTATTN_OK &&
+            rows64_sk_plan(p.B, p.Hq, p.Sq, p.Sk, pk.cu_count, &sk, &need) && need <= ws_bytes) {
+            sk.ws = static_cast<float*>(ws);
+            return f16 ? launch_rows64_sk<f16_t>(p, sk, stream) : launch_rows64_sk<bf16_t>(p, sk, stream);
+        }
+    }
     // grouped-query calls with groups of 4k heads and a positive scale take the persistent form
-    if (p.group >= 4 && p.group % 4 == 0 && p.q_and == 0xffffffffu && p.q_xor == 0u) {
+    if (gqa_form && positive) {
         int dev = 0;
         dtattn_device_peaks pk;
         if (rows64_stream_device(stream, &dev) == DTATTN_OK && dtattn_get_device_peaks(dev, &pk) == DTATTN_OK &&

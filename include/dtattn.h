@@ -97,7 +97,10 @@ typedef struct {
      * whose grid would leave CUs idle run the keys as several blocks in one launch and merge them by
      * LSE; the blocks' partial outputs live here.  Non-causal FP8 calls whose grid ends in a partly
      * empty round over the GPU's workgroup slots run that round's query blocks as key pieces, merged by
-     * a second launch; their partials live here.  dtattn_prefill_workspace_size() says
+     * a second launch; their partials live here.  Non-causal BF16/FP16 calls at D = Dv = 128 whose
+     * 256-row work items (groups not multiples of 4) would leave CUs idle run as equal shares of key
+     * tiles per CU, the items the shares cut merged by a second launch from records kept here.
+     * dtattn_prefill_workspace_size() says
      * how much a call can use; with less, the call runs unsplit (same results up to the rounding of the
      * partials). */
     void* workspace;
