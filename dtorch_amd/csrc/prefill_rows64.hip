@@ -450,22 +450,42 @@ __global__ void __launch_bounds__(256, 1) prefill_rows64_gqa_kernel(const Prefil
     }
 }
 
-// Stream-K form of the row layout (non-causal, positive scale).  A grid of n_items workgroups of 256 rows
-// (4 waves x 64 consecutive rows of one head) that does not fill whole rounds of the CUs leaves part of the
-// chip idle in its last round: C5a's 432 items on 256 CUs run as 1.69 rounds in the time of 2.  Here one
-// workgroup per CU takes an equal, contiguous share of all (item, key tile) units, items in order with the
-// query block fastest, and runs it as segments: whole items end in the usual epilogue, and the at most two
-// segments of a share that cut an item (its first and its last) leave their unnormalised O, row max and
-// row sums in a workspace record, which a second launch merges by the row maxima.  Shares are dealt XCD by
-// XCD (workgroup w on XCD w % 8 takes share (w % 8) G/8 + w / 8), so an XCD walks consecutive row blocks of
-// the same heads and their K/V stay in its L2.
+// Stream-K form of the persistent layouts (non-causal, positive scale).  Work items of the row layout (4 waves x
+// 64 consecutive rows of one head) or of the grouped-query form (the 4 query heads of a kv head over 64 rows)
+// run one workgroup per CU; a grid of items that does not fill whole rounds of the CUs leaves part of the chip
+// idle (128 items on 256 CUs: half of it).  Here each workgroup takes an equal, contiguous share of all (item,
+// key tile) units, items in order with the query block fastest, and runs it as segments: whole items end in
+// the usual epilogue, and the at most two segments of a share that cut an item (its first and its last) leave
+// O over their own row sums, the row maxima and the row sums in a workspace record, which a second launch
+// merges by the row maxima.  Shares are dealt XCD by XCD (workgroup w on XCD w % 8 takes share (w % 8) G/8 +
+// w / 8), so an XCD walks consecutive query blocks of the same heads and their K/V stay in its L2.
 struct Rows64Sk {
     int64_t units;  // n_items * nt
     int32_t nt;     // key tiles per item
-    int32_t nqb;    // 256-row query blocks per head
+    int32_t nqb;    // query blocks per item column: of 256 rows (row layout) or 64 rows (grouped-query form)
     int32_t G;      // workgroups (a multiple of 8)
     float* ws;      // 2 G records of kRows64SkRec floats
 };
+
+// Batch, query head and first row of wave `wave` in item i.  Row layout: 4 waves x 64 consecutive rows of one
+// head, items (b, hq, 256-row block).  Grouped-query form (GQA): the 4 query heads of one kv head over the
+// same 64 rows, items (b, kv head, 4-head subgroup, 64-row block).  The query block runs fastest in both.
+template <bool GQA>
+__device__ __forceinline__ void sk_item(const PrefillParams& p, const Rows64Sk& sk, int i, int wave, int* b,
+                                        int* hq, int* q0) {
+    const int qb = i % sk.nqb, rest = i / sk.nqb;
+    if constexpr (GQA) {
+        const int nsub = p.group / 4;
+        *b = rest / (p.Hkv * nsub);
+        const int r2 = rest % (p.Hkv * nsub);
+        *hq = (r2 / nsub) * p.group + (r2 % nsub) * 4 + wave;
+        *q0 = qb * 64;
+    } else {
+        *b = rest / p.Hq;
+        *hq = rest % p.Hq;
+        *q0 = qb * 256 + wave * 64;
+    }
+}
 // One record: lane l of wave w holds O / l of its 128 accumulators (the epilogue's order: float4 16 X + 4 dt + i4
 // at (32 w + 16 X + 4 dt + i4) 64 + l), then its rows' (max A, max B, sum A, sum B) at float4 4 * 64 * 32 + 64 w
 // + l.
@@ -473,7 +493,7 @@ constexpr int kRows64SkRec = 4 * 64 * 128 + 4 * 64 * 4;
 
 __device__ __forceinline__ int64_t sk_start(int64_t units, int G, int r) { return units * r / G; }
 
-template <typename T>
+template <typename T, bool GQA>
 __global__ void __launch_bounds__(256, 1) prefill_rows64_sk_kernel(const PrefillParams p, const Rows64Sk sk) {
     typedef typename Elem<T>::vec4 V4;
     constexpr int D = 128, BN = 64, DCH = 16, INSTR = 4;
@@ -515,11 +535,8 @@ __global__ void __launch_bounds__(256, 1) prefill_rows64_sk_kernel(const Prefill
         const int i = (int)(u / sk.nt);
         const int t0 = (int)(u - (int64_t)i * sk.nt);
         const int t1 = (int)min((int64_t)sk.nt, (int64_t)t0 + (u1 - u));
-        const int qb = i % sk.nqb, bh = i / sk.nqb;
-        s.b = bh / p.Hq;
-        s.hq = bh % p.Hq;
+        sk_item<GQA>(p, sk, i, wave, &s.b, &s.hq, &s.q0);
         const int hk = s.hq / p.group;
-        s.q0 = qb * 256 + wave * 64;
         s.nt = t1 - t0;
         s.skr = p.Sk - t0 * BN;
         s.whole = t0 == 0 && t1 == sk.nt;
@@ -688,7 +705,7 @@ __global__ void __launch_bounds__(256, 1) prefill_rows64_sk_kernel(const Prefill
 // boundary falls in (unless an earlier boundary falls in the same item), combining the records of every
 // share that covers part of it by their row maxima, in share order, then writes O and the LSE as the
 // epilogue of an uncut item would.
-template <typename T>
+template <typename T, bool GQA>
 __global__ void __launch_bounds__(256) rows64_sk_merge_kernel(const PrefillParams p, const Rows64Sk sk) {
     typedef typename Elem<T>::vec4 V4;
     constexpr int D = 128, DCH = 16;
@@ -732,9 +749,8 @@ __global__ void __launch_bounds__(256) rows64_sk_merge_kernel(const PrefillParam
         }
     }
     // the item's rows and head, as the main kernel derives them
-    const int qb = i % sk.nqb, bh = i / sk.nqb;
-    const int b = bh / p.Hq, hq = bh % p.Hq;
-    const int q0 = qb * 256 + wave * 64;
+    int b, hq, q0;
+    sk_item<GQA>(p, sk, i, wave, &b, &hq, &q0);
     T* Os = ostage + wave * 64 * D;
 #pragma unroll
     for (int X = 0; X < 2; ++X) {
@@ -814,10 +830,11 @@ static int launch_rows64_gqa(const PrefillParams& prm, int cus, hipStream_t stre
 // measured 16-27 on the shapes of the tests).  By it, 1 x 8 x 4096 (128 items on 256 CUs) gains 21% and
 // 1 x 24 x 4096 (384 items) 9%, while 1 x 24 x 4608 (432 items, 72 tiles each) keeps the plain grid: its
 // ragged round costs less than the records (stream-K measured 4-7% slower there).
-bool rows64_sk_plan(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int cus, Rows64Sk* sk, size_t* bytes) {
+bool rows64_sk_plan(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, bool gqa, int cus, Rows64Sk* sk, size_t* bytes) {
     const int G = cus & ~7;
     if (G < 8 || B <= 0 || Hq <= 0 || Sq <= 0 || Sk <= 0) return false;
-    const int64_t nqb = (Sq + 255) / 256, n_items = nqb * B * Hq, nt = (Sk + 63) / 64;
+    const int64_t nqb = gqa ? (Sq + 63) / 64 : (Sq + 255) / 256;
+    const int64_t n_items = nqb * B * (gqa ? Hq / 4 : Hq), nt = (Sk + 63) / 64;
     if (n_items > 0x7fffffff || n_items * nt > ((int64_t)1 << 40)) return false;
     const int64_t units = n_items * nt;
     const double per = (double)units / G;
@@ -835,29 +852,29 @@ bool rows64_sk_plan(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int cus, Rows
 }
 
 // Workspace the stream-K form can use for a prefill call on `device` (0: the call does not take it): bf16 /
-// fp16 at head dims D = Dv = 128, non-causal, no mask, a positive scale, groups that are not multiples of 4
-// (those take the grouped-query form), and tile offsets that fit the program's 32-bit arithmetic.
+// fp16 at head dims D = Dv = 128, non-causal, no mask, a positive scale, and tile offsets that fit the program's
+// 32-bit arithmetic; items of the row layout, or of the grouped-query form for groups of 4k heads.
 size_t rows64_sk_workspace(const dtattn_prefill_args* a, int device) {
     if (a->dtype != DTATTN_BF16 && a->dtype != DTATTN_FP16) return 0;
     if (a->D != 128 || a->Dv != 128 || a->causal != 0 || a->mask != nullptr || a->scale <= 0.f) return 0;
     if (a->Hkv <= 0 || a->Hq % a->Hkv != 0) return 0;
     const int64_t group = a->Hq / a->Hkv;
-    if (group >= 4 && group % 4 == 0) return 0;
+    const bool gqa = group >= 4 && group % 4 == 0;
     const int64_t ks = a->k_stride[2], vs = a->v_stride[2];
     if (ks < 0 || vs < 0 || (a->Sk + 128) * (ks > vs ? ks : vs) * 2 >= ((int64_t)1 << 31)) return 0;
     dtattn_device_peaks pk;
     if (dtattn_get_device_peaks(device, &pk) != DTATTN_OK) return 0;
     Rows64Sk sk;
     size_t bytes = 0;
-    return rows64_sk_plan(a->B, a->Hq, a->Sq, a->Sk, pk.cu_count, &sk, &bytes) ? bytes : 0;
+    return rows64_sk_plan(a->B, a->Hq, a->Sq, a->Sk, gqa, pk.cu_count, &sk, &bytes) ? bytes : 0;
 }
 
-template <typename T>
+template <typename T, bool GQA>
 static int launch_rows64_sk(const PrefillParams& p, const Rows64Sk& sk, hipStream_t stream) {
-    hipLaunchKernelGGL((prefill_rows64_sk_kernel<T>), dim3((unsigned)sk.G), dim3(256), 0, stream, p, sk);
+    hipLaunchKernelGGL((prefill_rows64_sk_kernel<T, GQA>), dim3((unsigned)sk.G), dim3(256), 0, stream, p, sk);
     const int st = check_launch("prefill_rows64_sk_kernel");
     if (st != DTATTN_OK) return st;
-    hipLaunchKernelGGL((rows64_sk_merge_kernel<T>), dim3((unsigned)(sk.G - 1)), dim3(256), 0, stream, p, sk);
+    hipLaunchKernelGGL((rows64_sk_merge_kernel<T, GQA>), dim3((unsigned)(sk.G - 1)), dim3(256), 0, stream, p, sk);
     return check_launch("rows64_sk_merge_kernel");
 }
 
@@ -866,15 +883,17 @@ static int launch_rows64_sk(const PrefillParams& p, const Rows64Sk& sk, hipStrea
 int prefill_rows64(const PrefillParams& p, bool causal, bool f16, void* ws, size_t ws_bytes, hipStream_t stream) {
     const bool positive = p.q_and == 0xffffffffu && p.q_xor == 0u;
     const bool gqa_form = p.group >= 4 && p.group % 4 == 0;
-    if (!causal && !gqa_form && positive && ws != nullptr && (reinterpret_cast<uintptr_t>(ws) & 255u) == 0) {
+    if (!causal && positive && ws != nullptr && (reinterpret_cast<uintptr_t>(ws) & 255u) == 0) {
         int dev = 0;
         dtattn_device_peaks pk;
         Rows64Sk sk;
         size_t need = 0;
         if (rows64_stream_device(stream, &dev) == DTATTN_OK && dtattn_get_device_peaks(dev, &pk) == DTATTN_OK &&
-            rows64_sk_plan(p.B, p.Hq, p.Sq, p.Sk, pk.cu_count, &sk, &need) && need <= ws_bytes) {
+            rows64_sk_plan(p.B, p.Hq, p.Sq, p.Sk, gqa_form, pk.cu_count, &sk, &need) && need <= ws_bytes) {
             sk.ws = static_cast<float*>(ws);
-            return f16 ? launch_rows64_sk<f16_t>(p, sk, stream) : launch_rows64_sk<bf16_t>(p, sk, stream);
+            if (gqa_form)
+                return f16 ? launch_rows64_sk<f16_t, true>(p, sk, stream) : launch_rows64_sk<bf16_t, true>(p, sk, stream);
+            return f16 ? launch_rows64_sk<f16_t, false>(p, sk, stream) : launch_rows64_sk<bf16_t, false>(p, sk, stream);
         }
     }
     // grouped-query calls with groups of 4k heads and a positive scale take the persistent form

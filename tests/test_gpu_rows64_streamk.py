@@ -1,14 +1,16 @@
 """GPU parity of the stream-K form of the head-dim-128 row layout (prefill_rows64_sk_kernel + its merge).
 
-Non-causal bf16/fp16 calls at D = 128 whose groups are not multiples of 4 (MHA included: the MMDiT joint
-attention of the reference's diffusers ports, python/dtorch/applications/huggingface/diffusers/models/
-attention_processor.py) run as 256-row work items, one workgroup per CU.  When those items do not fill
-whole rounds of the CUs, and the caller passes the workspace dtattn_prefill_workspace_size() asks for, each
-CU takes an equal share of all (item, key tile) units; items a share boundary cuts are finished from
-partial records by a second launch.  Checked against the same call without the workspace (the plain grid of
-prefill_rows64_kernel): rows of uncut items bit for bit, rows of cut items within 8e-3 on O and 1e-5 on the
-LSE, and both against the fp64 oracle on sampled rows; the split's run-to-run determinism; and that causal,
-grouped-query (groups of 4k) and whole-round calls plan no workspace.
+Non-causal bf16/fp16 calls at D = 128 run as work items of one workgroup per CU: 256 rows of one head (MHA
+and groups that are not multiples of 4, the MMDiT joint attention of the reference's diffusers ports among
+them: python/dtorch/applications/huggingface/diffusers/models/attention_processor.py), or the 4 query heads
+of a kv head over 64 rows (groups of 4k: the ring step's key blocks, python/dtorch/nn/
+scaled_dot_product_attention_with_cp.py:87-101).  When those items do not fill whole rounds of the CUs, and
+the caller passes the workspace dtattn_prefill_workspace_size() asks for, each CU takes an equal share of
+all (item, key tile) units; items a share boundary cuts are finished from partial records by a second
+launch.  Checked against the same call without the workspace (the plain grids of prefill_rows64_kernel and
+prefill_rows64_gqa_kernel): rows of uncut items bit for bit, rows of cut items within 8e-3 on O and 1e-5 on
+the LSE, and both against the fp64 oracle on sampled rows; the split's run-to-run determinism; and that
+causal, whole-round and C5a-shaped calls plan no workspace.
 """
 import ctypes
 
@@ -66,16 +68,29 @@ def _prefill(q, k, v, workspace):
     return o, lse
 
 
-def _cut_items(B, Hq, Sq, Sk, G):
-    """Indices of the 256-row items a share boundary cuts (the kernel's own partition)."""
-    nqb, nt = (Sq + 255) // 256, (Sk + 63) // 64
-    units = nqb * B * Hq * nt
-    cut = set()
-    for r in range(1, G):
-        u = units * r // G
-        if u % nt:
-            cut.add(u // nt)
-    return cut, nqb
+def _cut_rows(B, Hq, Hkv, Sq, Sk, G):
+    """Mask [B, Hq, Sq] of the rows of items a share boundary cuts (the kernel's own partition), and one cut
+    item's (b, heads, rows)."""
+    group = Hq // Hkv
+    gqa = group % 4 == 0
+    nqb, nt = ((Sq + 63) // 64 if gqa else (Sq + 255) // 256), (Sk + 63) // 64
+    units = nqb * B * (Hq // 4 if gqa else Hq) * nt
+    cut = sorted({units * r // G // nt for r in range(1, G) if (units * r // G) % nt})
+    mask = torch.zeros(B, Hq, Sq, dtype=torch.bool)
+    items = []
+    for i in cut:
+        qb, rest = i % nqb, i // nqb
+        if gqa:
+            nsub = group // 4
+            b, r2 = rest // (Hkv * nsub), rest % (Hkv * nsub)
+            heads = [(r2 // nsub) * group + (r2 % nsub) * 4 + w for w in range(4)]
+            rows = slice(qb * 64, min(Sq, qb * 64 + 64))
+        else:
+            b, heads, rows = rest // Hq, [rest % Hq], slice(qb * 256, min(Sq, qb * 256 + 256))
+        for h in heads:
+            mask[b, h, rows] = True
+        items.append((b, heads, rows))
+    return mask.cuda(), items
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,dtype", [
@@ -83,6 +98,9 @@ def _cut_items(B, Hq, Sq, Sk, G):
     (1, 8, 8, 4096, 4096, torch.bfloat16),    # 128 items: half the CUs idle on the plain grid
     (1, 12, 6, 2000, 5000, torch.bfloat16),   # groups of 2, ragged Sq and Sk (a tail tile of 8 keys)
     (2, 6, 6, 1500, 3000, torch.float16),     # fp16, two sequences
+    (1, 16, 4, 2048, 4096, torch.bfloat16),   # grouped-query form: 128 items of 4 heads x 64 rows
+    (1, 32, 8, 1000, 8192, torch.bfloat16),   # grouped-query form, ragged Sq (16 blocks, the last of 40 rows)
+    (2, 24, 3, 700, 6000, torch.float16),     # groups of 8 (two 4-head subgroups per kv head), fp16
 ])
 def test_streamk_against_plain_grid_and_oracle(B, Hq, Hkv, Sq, Sk, dtype):
     G = torch.cuda.get_device_properties(0).multi_processor_count & ~7
@@ -100,21 +118,17 @@ def test_streamk_against_plain_grid_and_oracle(B, Hq, Hkv, Sq, Sk, dtype):
     torch.cuda.synchronize()
     assert torch.equal(o, o2) and torch.equal(lse, lse2)
     assert torch.equal(fo, o) and torch.equal(flse, lse)  # the operator passes the workspace
-    cut, nqb = _cut_items(B, Hq, Sq, Sk, G)
-    assert cut, "no item was cut"
-    whole = torch.ones(B, Hq, Sq, dtype=torch.bool, device="cuda")
-    for i in cut:
-        qb, bh = i % nqb, i // nqb
-        whole[bh // Hq, bh % Hq, qb * 256:(qb + 1) * 256] = False
+    cutm, items = _cut_rows(B, Hq, Hkv, Sq, Sk, G)
+    assert items, "no item was cut"
+    whole = ~cutm
     assert torch.equal(o[whole], ou[whole]) and torch.equal(lse[whole], lseu[whole])
     assert not torch.equal(o[~whole], ou[~whole])  # the merge ran
     assert float((o.float() - ou.float()).abs().max()) <= 8e-3
     assert float(((lse - lseu).abs() / lseu.abs().clamp(min=1)).max()) <= 1e-5
     # rows of a cut item (its first and last rows) and of an uncut one, against the oracle
-    i = min(cut)
-    qb, bh = i % nqb, i // nqb
-    b, h = bh // Hq, bh % Hq
-    rows = np.unique(np.clip([qb * 256, qb * 256 + 100, qb * 256 + 255, 0, Sq - 1], 0, Sq - 1))
+    b, heads, rs = items[0]
+    h = heads[-1]
+    rows = np.unique(np.clip([rs.start, (rs.start + rs.stop) // 2, rs.stop - 1, 0, Sq - 1], 0, Sq - 1))
     qs = q[b:b + 1, h:h + 1, rows].float().cpu().double().numpy()
     hk = h // (Hq // Hkv)
     ks = k[b:b + 1, hk:hk + 1].float().cpu().double().numpy()
@@ -129,8 +143,6 @@ def test_streamk_not_planned():
     q = torch.randn(1, 24, 4608, 128, device=dev, dtype=torch.bfloat16)
     kv = torch.randn(1, 24, 4608, 128, device=dev, dtype=torch.bfloat16)
     assert _ws_bytes(q, kv, kv, causal=True) == 0                 # causal calls
-    kv8 = torch.randn(1, 6, 4608, 128, device=dev, dtype=torch.bfloat16)
-    assert _ws_bytes(q, kv8, kv8) == 0                            # groups of 4: the grouped-query form
     q16 = torch.randn(2, 32, 4096, 128, device=dev, dtype=torch.bfloat16)
     kv16 = torch.randn(2, 32, 4096, 128, device=dev, dtype=torch.bfloat16)
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
