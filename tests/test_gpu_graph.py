@@ -54,18 +54,20 @@ def test_decode_step_graph_replays_match_eager(dtype):
 
 
 @pytest.mark.parametrize("case", ["causal_gqa", "wide_key_blocks", "masked", "native_fp8", "native_fp8_tail",
-                                  "ring_step"])
+                                  "ring_step", "stream_k"])
 def test_prefill_graph_replays_match_eager(case):
     # The prefill entry points under capture, replayed with new inputs copied into the captured tensors:
     # every replay equals the eager call bit for bit.  The wide-head case takes the key-block split, so its
     # workspace and the LSE merge launch are captured too; the fp8 tail case (832 query blocks over 768 slots)
-    # takes the tail split and its merge launch.
+    # takes the tail split and its merge launch; the stream-K case (128 row-layout items on 256 CUs) its
+    # records in the workspace and their merge launch.
     import dtorch_amd.nn.functional as F
     rng = np.random.default_rng(sum(map(ord, case)))
     shapes = {"causal_gqa": (2, 8, 2, 300, 300, 128), "wide_key_blocks": (1, 2, 1, 256, 2048, 512),
               "masked": (1, 4, 4, 200, 260, 64), "native_fp8": (1, 4, 2, 256, 256, 128),
               "native_fp8_tail": (1, 32, 8, 3300, 2100, 128),
-              "ring_step": (1, 4, 2, 128, 256, 128)}  # a 128-row Q chunk against two 128-key chunks
+              "ring_step": (1, 4, 2, 128, 256, 128),  # a 128-row Q chunk against two 128-key chunks
+              "stream_k": (1, 8, 8, 4096, 4096, 128)}
     B, Hq, Hkv, Sq, Sk, D = shapes[case]
     mask = torch.from_numpy(rng.random((Sq, Sk)) < 0.7).cuda() if case == "masked" else None
     opt = F.SdpaOption(sage_attn_type="native_fp8") if case.startswith("native_fp8") else F.SdpaOption()
