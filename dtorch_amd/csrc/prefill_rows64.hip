@@ -464,7 +464,7 @@ struct Rows64Sk {
     int32_t nt;     // key tiles per item
     int32_t nqb;    // query blocks per item column: of 256 rows (row layout) or 64 rows (grouped-query form)
     int32_t G;      // workgroups (a multiple of 8)
-    float* ws;      // 2 G records of kRows64SkRec floats
+    char* ws;       // 2 G records of kRows64SkRec bytes
 };
 
 // Batch, query head and first row of wave `wave` in item i.  Row layout: 4 waves x 64 consecutive rows of one
@@ -486,10 +486,11 @@ __device__ __forceinline__ void sk_item(const PrefillParams& p, const Rows64Sk& 
         *q0 = qb * 256 + wave * 64;
     }
 }
-// One record: lane l of wave w holds O / l of its 128 accumulators (the epilogue's order: float4 16 X + 4 dt + i4
-// at (32 w + 16 X + 4 dt + i4) 64 + l), then its rows' (max A, max B, sum A, sum B) at float4 4 * 64 * 32 + 64 w
-// + l.
-constexpr int kRows64SkRec = 4 * 64 * 128 + 4 * 64 * 4;
+// One record: lane l of wave w holds O / l of its 128 accumulators in the input dtype, as the ring step's key
+// blocks and the reference's context-parallel merge keep partial outputs (the epilogue's order: 16-byte chunk
+// q = 8 X + 2 dt + i4 / 2 at (16 w + q) 64 + l), then, in fp32, its rows' (max A, max B, sum A, sum B) at byte
+// 65536 + 16 (64 w + l).
+constexpr int kRows64SkRec = 4 * 64 * 128 * 2 + 4 * 64 * 16;
 
 __device__ __forceinline__ int64_t sk_start(int64_t units, int G, int r) { return units * r / G; }
 
@@ -633,7 +634,7 @@ __global__ void __launch_bounds__(256, 1) prefill_rows64_sk_kernel(const Prefill
         }
         if (!cur.whole) {
             // a cut item: O over this segment's row sums, the row maxima and the row sums go to its record
-            f32x4* rec = reinterpret_cast<f32x4*>(sk.ws + (int64_t)cur.slot * kRows64SkRec);
+            char* rec = sk.ws + (int64_t)cur.slot * kRows64SkRec;
             float ls[2];
 #pragma unroll
             for (int X = 0; X < 2; ++X) {
@@ -643,18 +644,18 @@ __global__ void __launch_bounds__(256, 1) prefill_rows64_sk_kernel(const Prefill
 #pragma unroll
                 for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-                    for (int i4 = 0; i4 < 4; ++i4) {
-                        f32x4 v;
+                    for (int i8 = 0; i8 < 2; ++i8) {
+                        float v[8];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int kk = 16 * (dt & 1) + 4 * i4 + e;
+                        for (int e = 0; e < 8; ++e) {
+                            const int kk = 16 * (dt & 1) + 8 * i8 + e;
                             const float ov = X == 0 ? (dt < 2 ? OA01[kk] : OA23[kk]) : (dt < 2 ? OB01[kk] : OB23[kk]);
                             v[e] = ov * inv;
                         }
-                        rec[(32 * wave + 16 * X + 4 * dt + i4) * 64 + lane] = v;
+                        reinterpret_cast<u32x4*>(rec)[(16 * wave + 8 * X + 2 * dt + i8) * 64 + lane] = pack8<T>(v);
                     }
             }
-            rec[4 * 64 * 32 + 64 * wave + lane] = f32x4{mA, mB, ls[0], ls[1]};
+            reinterpret_cast<f32x4*>(rec + 65536)[64 * wave + lane] = f32x4{mA, mB, ls[0], ls[1]};
             if (!more) break;
             continue;
         }
@@ -730,8 +731,8 @@ __global__ void __launch_bounds__(256) rows64_sk_merge_kernel(const PrefillParam
     for (int k = 0; k < 128; ++k) o[k] = 0.f;
     for (int q = r - 1; q < G && sk_start(sk.units, G, q) < ie; ++q) {
         const int slot = 2 * q + ((q == r - 1 && sk_start(sk.units, G, q) < ib) ? 1 : 0);
-        const f32x4* rec = reinterpret_cast<const f32x4*>(sk.ws + (int64_t)slot * kRows64SkRec);
-        const f32x4 ml = rec[4 * 64 * 32 + 64 * wave + lane];
+        const char* rec = sk.ws + (int64_t)slot * kRows64SkRec;
+        const f32x4 ml = reinterpret_cast<const f32x4*>(rec + 65536)[64 * wave + lane];
         const float nA = fmaxf(mA, ml[0]), nB = fmaxf(mB, ml[1]);
         // a max of -inf carries no keys: weight 0
         const float aA = mA == kNegInf ? 0.f : exp2f(mA - nA), bA = ml[0] == kNegInf ? 0.f : ml[2] * exp2f(ml[0] - nA);
@@ -741,11 +742,12 @@ __global__ void __launch_bounds__(256) rows64_sk_merge_kernel(const PrefillParam
         mA = nA;
         mB = nB;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            const f32x4 v = rec[(32 * wave + j) * 64 + lane];
-            const float a = j < 16 ? aA : aB, w = j < 16 ? bA : bB;
+        for (int c = 0; c < 16; ++c) {
+            float v[8];
+            unpack8<T>(reinterpret_cast<const u32x4*>(rec)[(16 * wave + c) * 64 + lane], v);
+            const float a = c < 8 ? aA : aB, w = c < 8 ? bA : bB;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[4 * j + e] = o[4 * j + e] * a + v[e] * w;
+            for (int e = 0; e < 8; ++e) o[8 * c + e] = o[8 * c + e] * a + v[e] * w;
         }
     }
     // the item's rows and head, as the main kernel derives them
@@ -823,13 +825,13 @@ static int launch_rows64_gqa(const PrefillParams& prm, int cus, hipStream_t stre
     return check_launch("prefill_rows64_gqa_kernel");
 }
 
-// Shares of the stream-K form for a non-causal row-layout call (B, Hq, Sq, Sk) on `cus` CUs, and the workspace
-// its records need; false unless the model below says the shares beat the plain grid by 5%.  Times in key
-// tiles (of 256 rows x 64 keys on every CU): an item costs nt + 4 (Q load, first tiles, epilogue); a share
-// its tiles plus 4 per segment, plus 20 for writing and merging the records (~68 MB of fp32 at 256 CUs;
-// measured 16-27 on the shapes of the tests).  By it, 1 x 8 x 4096 (128 items on 256 CUs) gains 21% and
-// 1 x 24 x 4096 (384 items) 9%, while 1 x 24 x 4608 (432 items, 72 tiles each) keeps the plain grid: its
-// ragged round costs less than the records (stream-K measured 4-7% slower there).
+// Shares of the stream-K form for a non-causal call (B, Hq, Sq, Sk; grouped-query items when gqa) on `cus` CUs,
+// and the workspace its records need; false unless the model below says the shares beat the plain grid by 5%.
+// Times in key tiles (of 64 keys for every wave of a CU): an item costs nt + 4 (Q load, first tiles, epilogue);
+// a share its tiles plus 4 per segment, plus 14 for writing and merging the records (~36 MB at 256 CUs;
+// measured 13-20 on the shapes of the tests).  By it, 1 x 8 x 4096 (128 items on 256 CUs) gains 26-30% and
+// 1 x 24 x 4096 (384 items) 10%, while 1 x 24 x 4608 (432 items of 72 tiles) keeps the plain grid, where
+// stream-K measured 1-3% slower.
 bool rows64_sk_plan(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, bool gqa, int cus, Rows64Sk* sk, size_t* bytes) {
     const int G = cus & ~7;
     if (G < 8 || B <= 0 || Hq <= 0 || Sq <= 0 || Sk <= 0) return false;
@@ -841,13 +843,13 @@ bool rows64_sk_plan(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, bool gqa, int
     if (per < 8.0) return false;
     const double plain = (double)((n_items + G - 1) / G) * (double)(nt + 4);
     const double segs = std::ceil(per / (double)nt) + 1.0;
-    if (std::ceil(per) + 4.0 * segs + 20.0 >= 0.95 * plain) return false;
+    if (std::ceil(per) + 4.0 * segs + 14.0 >= 0.95 * plain) return false;
     sk->units = units;
     sk->nt = (int32_t)nt;
     sk->nqb = (int32_t)nqb;
     sk->G = G;
     sk->ws = nullptr;
-    *bytes = (size_t)2 * G * kRows64SkRec * sizeof(float);
+    *bytes = (size_t)2 * G * kRows64SkRec;
     return true;
 }
 
@@ -890,7 +892,7 @@ int prefill_rows64(const PrefillParams& p, bool causal, bool f16, void* ws, size
         size_t need = 0;
         if (rows64_stream_device(stream, &dev) == DTATTN_OK && dtattn_get_device_peaks(dev, &pk) == DTATTN_OK &&
             rows64_sk_plan(p.B, p.Hq, p.Sq, p.Sk, gqa_form, pk.cu_count, &sk, &need) && need <= ws_bytes) {
-            sk.ws = static_cast<float*>(ws);
+            sk.ws = static_cast<char*>(ws);
             if (gqa_form)
                 return f16 ? launch_rows64_sk<f16_t, true>(p, sk, stream) : launch_rows64_sk<bf16_t, true>(p, sk, stream);
             return f16 ? launch_rows64_sk<f16_t, false>(p, sk, stream) : launch_rows64_sk<bf16_t, false>(p, sk, stream);

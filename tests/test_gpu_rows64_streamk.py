@@ -6,8 +6,9 @@ them: python/dtorch/applications/huggingface/diffusers/models/attention_processo
 of a kv head over 64 rows (groups of 4k: the ring step's key blocks, python/dtorch/nn/
 scaled_dot_product_attention_with_cp.py:87-101).  When those items do not fill whole rounds of the CUs, and
 the caller passes the workspace dtattn_prefill_workspace_size() asks for, each CU takes an equal share of
-all (item, key tile) units; items a share boundary cuts are finished from partial records by a second
-launch.  Checked against the same call without the workspace (the plain grids of prefill_rows64_kernel and
+all (item, key tile) units; items a share boundary cuts are finished by a second launch from partial records
+(O over the piece's row sums in the input dtype, as the ring step's blocks keep it, and fp32 row maxima and
+sums).  Checked against the same call without the workspace (the plain grids of prefill_rows64_kernel and
 prefill_rows64_gqa_kernel): rows of uncut items bit for bit, rows of cut items within 8e-3 on O and 1e-5 on
 the LSE, and both against the fp64 oracle on sampled rows; the split's run-to-run determinism; and that
 causal, whole-round and C5a-shaped calls plan no workspace.
@@ -150,4 +151,4 @@ def test_streamk_not_planned():
     q64 = torch.randn(1, 24, 4608, 64, device=dev, dtype=torch.bfloat16)
     assert _ws_bytes(q64, q64, q64) == 0                          # head dim 64
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
-        assert _ws_bytes(q, kv, kv) == 0  # 432 items of 72 tiles: the records would cost more than the last round
+        assert _ws_bytes(q, kv, kv) == 0  # C5a: 432 items of 72 tiles, the records cost what the last round saves
