@@ -152,3 +152,25 @@ def test_streamk_not_planned():
     assert _ws_bytes(q64, q64, q64) == 0                          # head dim 64
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
         assert _ws_bytes(q, kv, kv) == 0  # C5a: 432 items of 72 tiles, the records cost what the last round saves
+
+
+def test_streamk_strided_layout_and_no_lse():
+    # [B, S, H, D] storage (row pitch H * D) and the one-output operator (no LSE pointer: the records still
+    # carry the row sums, the merge writes O alone); the result equals the plain grid on uncut rows
+    import dtorch_amd.nn.functional as F
+    G = torch.cuda.get_device_properties(0).multi_processor_count & ~7
+    g = torch.Generator(device="cuda").manual_seed(77)
+    B, Hq, Hkv, Sq, Sk = 1, 12, 6, 2000, 5000
+    q = torch.randn(B, Sq, Hq, 128, generator=g, device="cuda").to(torch.bfloat16).transpose(1, 2)
+    k = torch.randn(B, Sk, Hkv, 128, generator=g, device="cuda").to(torch.bfloat16).transpose(1, 2)
+    v = torch.randn(B, Sk, Hkv, 128, generator=g, device="cuda").to(torch.bfloat16).transpose(1, 2)
+    assert _ws_bytes(q, k, v) > 0, "no stream-K plan"
+    o = F.scaled_dot_product_attention(q, k, v, enable_gqa=True)
+    o_lse, _ = F.scaled_dot_product_attention_with_lse(q, k, v, enable_gqa=True)
+    ou, _ = _prefill(q, k, v, False)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_lse)
+    cutm, items = _cut_rows(B, Hq, Hkv, Sq, Sk, G)
+    assert items
+    assert torch.equal(o[~cutm], ou[~cutm])
+    assert float((o.float() - ou.float()).abs().max()) <= 8e-3
