@@ -486,8 +486,8 @@ __device__ __forceinline__ void sk_item(const PrefillParams& p, const Rows64Sk& 
         *q0 = qb * 256 + wave * 64;
     }
 }
-// One record: lane l of wave w holds O / l of its 128 accumulators in the input dtype, as the ring step's key
-// blocks and the reference's context-parallel merge keep partial outputs (the epilogue's order: 16-byte chunk
+// One record: lane l of wave w holds O / l of its 128 accumulators in the input dtype, as the blockwise ring
+// step keeps its key blocks' outputs before their LSE merge (the epilogue's order: 16-byte chunk
 // q = 8 X + 2 dt + i4 / 2 at (16 w + q) 64 + l), then, in fp32, its rows' (max A, max B, sum A, sum B) at byte
 // 65536 + 16 (64 w + l).
 constexpr int kRows64SkRec = 4 * 64 * 128 * 2 + 4 * 64 * 16;
