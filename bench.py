@@ -171,6 +171,29 @@ def cpu_rate(torch, name, fn, flops, min_seconds, sample, min_reps=3):
             "logical_cpus": os.cpu_count(), "sample": sample}
 
 
+def _prefill_plain(q, k, v):
+    """Non-causal bf16/fp16 prefill through the C ABI with no workspace: the plain grid of work items."""
+    import ctypes
+    import torch
+    from dtorch_amd import _lib
+    o = torch.empty(q.shape[:3] + (v.shape[3],), dtype=q.dtype, device=q.device)
+    lse = torch.empty(q.shape[:3], device=q.device)
+    a = _lib.PrefillArgs()
+    a.q, a.k, a.v, a.o, a.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr()
+    a.B, a.Hq, a.Sq, a.D = q.shape
+    a.Hkv, a.Sk, a.Dv = k.shape[1], k.shape[2], v.shape[3]
+    for dst, t in ((a.q_stride, q), (a.k_stride, k), (a.v_stride, v), (a.o_stride, o)):
+        dst[0], dst[1], dst[2] = t.stride(0), t.stride(1), t.stride(2)
+    a.lse_stride[0], a.lse_stride[1] = lse.stride(0), lse.stride(1)
+    a.dtype = a.o_dtype = 0 if q.dtype == torch.bfloat16 else 1
+    lib = _lib.cabi()
+    lib.dtattn_prefill_fwd.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    st = lib.dtattn_prefill_fwd(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    if st != 0:
+        raise RuntimeError(f"dtattn_prefill_fwd failed ({st})")
+    return o, lse
+
+
 def secondary_workloads(torch, F, dev, timer, cpu_info=None, cpu_seconds=0.0):
     extras = {}
     # Cache flush between decode reps: READ 1 GiB (more than the 8 x 4 MB L2 plus the 256 MB MALL), so
@@ -316,6 +339,16 @@ def secondary_workloads(torch, F, dev, timer, cpu_info=None, cpu_seconds=0.0):
     med, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(q5, k5, v5), reps=10, batch=4)
     extras["mmdit_c5a_bf16"] = {"TFLOP/s": round(f5 / med / 1e12, 1), "frac_bf16": round(f5 / med / PEAK_BF16, 4),
                                 "us": round(med * 1e6, 1)}
+    # a non-causal call with fewer 256-row work items than CUs (8 heads of 4096): the operator's workspace
+    # runs it as stream-K shares; the same call with the plain grid for comparison (the C ABI without one)
+    qs, ks, vs = (torch.randn(1, 8, 4096, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    fs = 4 * 8 * 128 * 4096 * 4096
+    med_s, _ = timer.run(lambda: F.scaled_dot_product_attention_with_lse(qs, ks, vs), reps=10, batch=4)
+    med_p, _ = timer.run(lambda: _prefill_plain(qs, ks, vs), reps=10, batch=4)
+    extras["prefill_streamk_1x8x4096"] = {"TFLOP/s": round(fs / med_s / 1e12, 1), "us": round(med_s * 1e6, 1),
+                                          "plain_grid_TFLOP/s": round(fs / med_p / 1e12, 1),
+                                          "note": "128 items of 256 rows on 256 CUs: stream-K shares vs the plain grid"}
+    log(f"non-causal 1x8x4096: stream-K {fs / med_s / 1e12:.0f} TFLOP/s, plain grid {fs / med_p / 1e12:.0f} TFLOP/s")
     # fp8: the native_fp8 op end to end (per-head quantization of q, k, v plus the attention, three
     # launches and the tail merge), and the attention alone on codes quantized beforehand (the codes entry
     # point: the attention kernel and the tail merge)
