@@ -180,8 +180,9 @@ class Program:
                     self.e(*self.vread(vpre, g))
             self.e(*sl[m])
 
-    def phase_b(self, sc, sn, vb, chunks, with_max, pre):
-        """O += V(buffer vb)^T P, with the VALU of P chunks from S[sc] and (with_max) the row max of S[sn]."""
+    def phase_b(self, sc, sn, vb, chunks, with_max, pre, skip=()):
+        """O += V(buffer vb)^T P, with the VALU of P chunks from S[sc] and (with_max) the row max of S[sn].
+        The MFMAs of the P chunks in `skip` (all of whose scores are masked, so P = 0) are left out."""
         valu, done = [], {}
         for X, ks in chunks:
             valu += self.chunk(sc, X, ks)
@@ -198,7 +199,8 @@ class Program:
             if m % 2 == 0:
                 self.e(f"s_waitcnt lgkmcnt({2 * min(3, 15 - g)})")
             o = ar(O(X, dt), 16)
-            self.e(f"{self.mfma} {o}, {vr(T((g + 1) % NT), 4)}, {vr(P(X, ks), 4)}, {o}")
+            if (X, ks) not in skip:
+                self.e(f"{self.mfma} {o}, {vr(T((g + 1) % NT), 4)}, {vr(P(X, ks), 4)}, {o}")
             if m % 2 == 1 and g + 4 < 16:
                 self.e(*self.vread(vb, g + 4))
             self.e(*sl[m])
@@ -294,8 +296,18 @@ class Program:
         self.rescale(1, f"{lb}_rb")
         self.e(f"s_branch {lb}_next", f"{lb}_last:", *flat)
         # the wave's last tile: P(t) and O += V(t)^T P(t) only
+        if self.causal:
+            # On a causal diagonal, block A may see none of the tile's upper 32 keys (every lane's limit
+            # below offset 32): its P chunks 2-3 are then exp2(-inf) = 0, adding +0 to the row sums and
+            # nothing to O, so their VALU and MFMAs are skipped.
+            self.e("s_lshl_b32 s42, s40, 6", f"v_subrev_u32 v{RT}, s42, v{self.lb}",
+                   f"v_cmp_gt_i32 vcc, 32, v{RT}", "s_cmp_eq_u64 vcc, exec", f"s_cbranch_scc1 {lb}_diag")
         self.e(*[x for X, ks in ca for x in self.chunk(par, X, ks)])
         self.phase_b(par, 1 - par, par, cb, False, False)
+        if self.causal:
+            self.e(f"s_branch {lb}_next", f"{lb}_diag:")
+            self.e(*[x for X, ks in ca for x in self.chunk(par, X, ks)])
+            self.phase_b(par, 1 - par, par, cb[1:2] + cb[3:], False, False, skip=((0, 2), (0, 3)))
         self.e(f"{lb}_next:", "s_add_i32 s40, s40, 1")
 
     def program(self):
